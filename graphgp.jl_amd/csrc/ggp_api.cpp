@@ -1,0 +1,868 @@
+// ggp_api.cpp — the C ABI of libgraphgp_hip (declared in include/graphgp_hip.h).
+//
+// Each op runs as: a fully parallel factor pass over all refined points (mean_vec, std — the
+// value-independent part of every per-point kernel of the reference) on the main stream, the
+// dense first layer on a side stream at the same time, then the sequential depth-level sweeps
+// and the parallel adjoint passes. Ops return after the work is done; a failed dense
+// factorization is detected there and retried with escalating jitter, as src/dense.jl:46-67.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/graphgp_hip.h"
+#include "ggp_internal.h"
+
+using namespace ggp;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+#define HC(x)                                                                                  \
+    do {                                                                                       \
+        hipError_t e_ = (x);                                                                   \
+        if (e_ != hipSuccess)                                                                  \
+            return fail(GGP_ERR_HIP, std::string(#x) + ": " + hipGetErrorString(e_));         \
+    } while (0)
+
+bool supported_k(int64_t k) { return k == 4 || k == 8 || k == 10 || k == 16; }
+bool supported_d(int64_t d) { return d >= 2 && d <= 4; }
+
+}  // namespace
+
+struct ggp_graph {
+    int dtype = GGP_F32;
+    int dev = 0;
+    int ncu = 256;
+    size_t lds_max = 65536;
+    Graph g;
+    Table<float> tf;
+    Table<double> td;
+    bool has_cov = false;
+    unsigned nblk_factor = 1024, nblk_pull = 512;
+    int nw_dense = 256;
+    hipStream_t s_main = nullptr, s_side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_user = nullptr;
+    // workspaces (element type T = dtype)
+    void *mv = nullptr, *sd = nullptr, *v = nullptr, *xt = nullptr, *vb = nullptr,
+         *vbt = nullptr, *xg = nullptr, *A = nullptr, *tmp = nullptr;
+    double* scal_partial = nullptr;  // nblk_factor (>= nblk_pull) doubles
+    double* dscal = nullptr;         // 8 doubles
+    double* hscal = nullptr;         // pinned host mirror of dscal
+    int* info = nullptr;
+    int* hinfo = nullptr;            // pinned host mirror of info
+    double* hist = nullptr;          // (nblk_pull + nw_dense) x nb
+    int hist_nb = 0;
+    double *W = nullptr, *C = nullptr, *Q = nullptr, *u = nullptr;  // dense f64 scratch (lazy)
+    std::vector<void*> owned;
+    // optional HIP-event timers around the main kernels (ggp_kernel_timers)
+    bool timing = false;
+    hipEvent_t tev[2 * 8] = {};
+    bool tpending[8] = {};
+    double tms[8] = {};
+    int64_t tcnt[8] = {};
+};
+
+namespace {
+
+template <typename T> Table<T>& table(ggp_graph* h);
+template <> Table<float>& table<float>(ggp_graph* h) { return h->tf; }
+template <> Table<double>& table<double>(ggp_graph* h) { return h->td; }
+
+int dmalloc(ggp_graph* h, void** p, size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        *p = nullptr;
+        return fail(GGP_ERR_HIP, std::string("hipMalloc: ") + hipGetErrorString(e));
+    }
+    h->owned.push_back(*p);
+    return 0;
+}
+
+void free_all(ggp_graph* h) {
+    for (void* p : h->owned) (void)hipFree(p);
+    h->owned.clear();
+    if (h->hscal) (void)hipHostFree(h->hscal);
+    if (h->hinfo) (void)hipHostFree(h->hinfo);
+    if (h->s_main) (void)hipStreamDestroy(h->s_main);
+    if (h->s_side) (void)hipStreamDestroy(h->s_side);
+    if (h->ev_fork) (void)hipEventDestroy(h->ev_fork);
+    if (h->ev_join) (void)hipEventDestroy(h->ev_join);
+    if (h->ev_user) (void)hipEventDestroy(h->ev_user);
+    for (int i = 0; i < 16; ++i)
+        if (h->tev[i]) (void)hipEventDestroy(h->tev[i]);
+}
+
+// ---- covariance table ----------------------------------------------------------------------
+template <typename T> struct Bits;
+template <> struct Bits<float> {
+    using U = uint32_t;
+    static U of(float x) { U u; std::memcpy(&u, &x, 4); return u; }
+    static float from(U u) { float x; std::memcpy(&x, &u, 4); return x; }
+};
+template <> struct Bits<double> {
+    using U = uint64_t;
+    static U of(double x) { U u; std::memcpy(&u, &x, 8); return u; }
+    static double from(U u) { double x; std::memcpy(&x, &u, 8); return x; }
+};
+
+template <typename T>
+int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
+    if (nb < 2) return fail(GGP_ERR_ARG, "nbins must be >= 2");
+    if (nb > 65535) return fail(GGP_ERR_ARG, "nbins must be < 65536");
+    for (int64_t i = 0; i < nb; ++i) {
+        if (!std::isfinite(bins[i]) || !std::isfinite(vals[i]))
+            return fail(GGP_ERR_ARG, "bins and vals must be finite");
+        if (i > 0 && !(bins[i] > bins[i - 1]))
+            return fail(GGP_ERR_ARG, "bins must be strictly increasing");
+    }
+    if (!(bins[0] >= T(0))) return fail(GGP_ERR_ARG, "bins[0] must be >= 0");
+    Table<T>& tb = table<T>(h);
+    // Segment entries; slope evaluated exactly as src/interp.jl:30 does inline.
+    std::vector<TabEnt<T>> ent((size_t)nb - 1);
+    for (int64_t i = 0; i + 1 < nb; ++i) {
+        ent[i].x0 = bins[i];
+        ent[i].y0 = vals[i];
+        ent[i].x1 = bins[i + 1];
+        volatile T dy = vals[i + 1] - vals[i];
+        volatile T dx = bins[i + 1] - bins[i];
+        ent[i].slope = dy / dx;
+    }
+    // Cell index over bit patterns from bins[1] to bins[nb-1].
+    using U = typename Bits<T>::U;
+    const U base = Bits<T>::of(bins[1]);
+    const U range = Bits<T>::of(bins[nb - 1]) - base;
+    const size_t entb = (size_t)(nb - 1) * sizeof(TabEnt<T>);
+    size_t budget = h->lds_max > entb + (size_t)nb * 8 + 512 ? h->lds_max - entb - (size_t)nb * 8 - 512 : 0;
+    int64_t umax = std::min<int64_t>(4096, (int64_t)(budget / 2) - 1);
+    if (umax < 1) return fail(GGP_ERR_ARG, "covariance table too large for LDS");
+    int shift = 0;
+    while ((int64_t)(range >> shift) + 1 > umax) ++shift;
+    const int ucells = (int)((range >> shift) + 1);
+    std::vector<uint16_t> acc((size_t)ucells + 1);
+    acc[0] = 0;
+    int64_t lo = 1;
+    for (int c = 0; c < ucells; ++c) {
+        const T cm = Bits<T>::from(base + ((U)c << shift));
+        while (lo + 1 <= nb - 2 && bins[lo + 1] <= cm) ++lo;
+        acc[(size_t)c + 1] = (uint16_t)std::min<int64_t>(lo, nb - 2);
+    }
+    TabParams<T> P{};
+    P.b0 = bins[0];
+    P.b1 = bins[1];
+    P.bl = bins[nb - 1];
+    P.v0 = vals[0];
+    P.vl = vals[nb - 1];
+    P.base = base;
+    P.shift = shift;
+    P.ucells = ucells;
+    P.nb = (int)nb;
+    const bool realloc_tab = !tb.tab || tb.P.nb != (int)nb || tb.P.ucells != ucells;
+    if (realloc_tab) {
+        if (dmalloc(h, (void**)&tb.tab, entb)) return GGP_ERR_HIP;
+        if (dmalloc(h, (void**)&tb.acc, acc.size() * sizeof(uint16_t))) return GGP_ERR_HIP;
+        if (!tb.params && dmalloc(h, (void**)&tb.params, sizeof(TabParams<T>))) return GGP_ERR_HIP;
+    }
+    HC(hipMemcpy(tb.tab, ent.data(), entb, hipMemcpyHostToDevice));
+    HC(hipMemcpy(tb.acc, acc.data(), acc.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
+    HC(hipMemcpy(tb.params, &P, sizeof(P), hipMemcpyHostToDevice));
+    tb.P = P;
+    tb.bins.assign(bins, bins + nb);
+    tb.vals.assign(vals, vals + nb);
+    if (h->hist_nb != (int)nb) {
+        if (dmalloc(h, (void**)&h->hist,
+                    (size_t)(h->nblk_pull + h->nw_dense) * (size_t)nb * sizeof(double)))
+            return GGP_ERR_HIP;
+        h->hist_nb = (int)nb;
+    }
+    h->has_cov = true;
+    return 0;
+}
+
+// ---- kernel timers ---------------------------------------------------------------------------
+enum Timer { TM_FACTOR = 0, TM_PULLBACK = 1, TM_SWEEP_FWD = 2, TM_SWEEP_REV = 3, TM_DENSE = 4,
+             TM_OP = 5, TM_COUNT = 6 };
+const char* const kTimerNames[TM_COUNT] = {"factor", "pullback", "sweep_fwd", "sweep_rev",
+                                           "dense", "op"};
+
+inline void tstart(ggp_graph* h, int t, hipStream_t st) {
+    if (h->timing) (void)hipEventRecord(h->tev[2 * t], st);
+}
+inline void tstop(ggp_graph* h, int t, hipStream_t st) {
+    if (h->timing) {
+        (void)hipEventRecord(h->tev[2 * t + 1], st);
+        h->tpending[t] = true;
+    }
+}
+void tcollect(ggp_graph* h) {
+    if (!h->timing) return;
+    for (int t = 0; t < TM_COUNT; ++t)
+        if (h->tpending[t]) {
+            float ms = 0.f;
+            if (hipEventElapsedTime(&ms, h->tev[2 * t], h->tev[2 * t + 1]) == hipSuccess) {
+                h->tms[t] += ms;
+                h->tcnt[t] += 1;
+            }
+            h->tpending[t] = false;
+        }
+}
+
+// ---- stream plumbing -------------------------------------------------------------------------
+int enter(ggp_graph* h, hipStream_t user) {
+    HC(hipSetDevice(h->dev));
+    HC(hipEventRecord(h->ev_user, user));
+    HC(hipStreamWaitEvent(h->s_main, h->ev_user, 0));
+    tstart(h, TM_OP, h->s_main);
+    return 0;
+}
+int fork(ggp_graph* h) {
+    HC(hipEventRecord(h->ev_fork, h->s_main));
+    HC(hipStreamWaitEvent(h->s_side, h->ev_fork, 0));
+    return 0;
+}
+int join(ggp_graph* h) {
+    HC(hipEventRecord(h->ev_join, h->s_side));
+    HC(hipStreamWaitEvent(h->s_main, h->ev_join, 0));
+    return 0;
+}
+// Drain the main stream, release the user stream, and fetch info + scalars.
+int finish(ggp_graph* h, hipStream_t user) {
+    HC(hipMemcpyAsync(h->hinfo, h->info, sizeof(int), hipMemcpyDeviceToHost, h->s_main));
+    HC(hipMemcpyAsync(h->hscal, h->dscal, 8 * sizeof(double), hipMemcpyDeviceToHost, h->s_main));
+    HC(hipGetLastError());
+    tstop(h, TM_OP, h->s_main);
+    HC(hipEventRecord(h->ev_user, h->s_main));
+    HC(hipStreamWaitEvent(user, h->ev_user, 0));
+    HC(hipStreamSynchronize(h->s_main));
+    tcollect(h);
+    return 0;
+}
+
+template <typename T> T* tp(void* p) { return static_cast<T*>(p); }
+
+// Dense factor with jitter escalation (src/dense.jl:46-67), synchronous; used after the first
+// in-op attempt reported a non-positive pivot.
+template <typename T>
+int dense_retry(ggp_graph* h) {
+    const Table<T>& tb = table<T>(h);
+    const int n = (int)h->g.n0;
+    T dmean = T(0);
+    for (int i = 0; i < n; ++i) dmean += tb.vals[0];  // every diagonal entry is vals[1]
+    dmean = dmean / T(n > 1 ? n : 1);
+    T e = T(1e-9);
+    while (e <= T(1e-2)) {
+        launch_fill<int>(h->info, 0, 1, h->s_main);
+        dense_assemble<T>(h->g, tb, tp<T>(h->A), e * dmean, h->s_main);
+        dense_potrf<T>(tp<T>(h->A), n, h->info, h->s_main);
+        HC(hipMemcpyAsync(h->hinfo, h->info, sizeof(int), hipMemcpyDeviceToHost, h->s_main));
+        HC(hipStreamSynchronize(h->s_main));
+        if (*h->hinfo == 0) return 0;
+        e *= T(10);
+    }
+    return fail(GGP_ERR_NOT_PD,
+                "dense first-layer covariance is not positive definite even with 1e-2 relative "
+                "jitter; increase the kernel jitter or reduce n0");
+}
+
+template <typename T>
+void dense_factor_async(ggp_graph* h, hipStream_t st) {
+    tstart(h, TM_DENSE, st);
+    launch_fill<int>(h->info, 0, 1, st);
+    dense_assemble<T>(h->g, table<T>(h), tp<T>(h->A), T(0), st);
+    dense_potrf<T>(tp<T>(h->A), (int)h->g.n0, h->info, st);
+    tstop(h, TM_DENSE, st);
+}
+
+// Factor / pullback launches bracketed by the timers.
+template <typename T>
+void factor_t(ggp_graph* h, int mode, T* mv, T* sd, T* terms, double* partial, const T* values,
+              T* xi_out) {
+    tstart(h, TM_FACTOR, h->s_main);
+    launch_factor<T>(h->g, table<T>(h), mode, mv, sd, terms, partial, values, xi_out,
+                     h->nblk_factor, h->s_main);
+    tstop(h, TM_FACTOR, h->s_main);
+}
+template <typename T>
+void pullback_t(ggp_graph* h, int mode, const T* v, const T* xi, const T* vb) {
+    tstart(h, TM_PULLBACK, h->s_main);
+    launch_pullback<T>(h->g, table<T>(h), mode, v, xi, vb, h->hist, h->scal_partial, h->nblk_pull,
+                       h->s_main);
+    tstop(h, TM_PULLBACK, h->s_main);
+}
+
+int ensure_dense64(ggp_graph* h) {
+    if (h->W) return 0;
+    // the inverse kernel keeps one column of L^-1 (n0 doubles) in LDS
+    if ((size_t)h->g.n0 * sizeof(double) > h->lds_max)
+        return fail(GGP_ERR_ARG, "dense-layer gradients support n0 up to lds/8 (8192)");
+    const size_t nn = (size_t)h->g.n0 * (size_t)h->g.n0 * sizeof(double);
+    if (dmalloc(h, (void**)&h->W, nn) || dmalloc(h, (void**)&h->C, nn) ||
+        dmalloc(h, (void**)&h->Q, nn) || dmalloc(h, (void**)&h->u, (size_t)h->g.n0 * 8))
+        return GGP_ERR_HIP;
+    return 0;
+}
+
+int check_ready(ggp_graph* h) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    if (!h->has_cov) return fail(GGP_ERR_NO_COV, "no covariance table: call ggp_set_cov_iso first");
+    return 0;
+}
+
+// Forward sweep over all depth levels (src/api.jl:126-137); xi indexed as xi[xi_off + m].
+template <typename T>
+void sweep_forward(ggp_graph* h, T* v, const T* xi, int64_t xi_off, hipStream_t st) {
+    const Graph& g = h->g;
+    tstart(h, TM_SWEEP_FWD, st);
+    for (size_t b = 1; b < g.offsets.size(); ++b) {
+        const int64_t len = g.offsets[b] - g.offsets[b - 1];
+        if (len <= 0) continue;
+        launch_sweep_fwd<T>(g, v, xi, xi_off, tp<T>(h->mv), tp<T>(h->sd), g.offsets[b - 1] - g.n0,
+                            len, st);
+    }
+    tstop(h, TM_SWEEP_FWD, st);
+}
+
+// Reverse sweep, latest level first, then the dense level (src/grad.jl:433-445, 483-489).
+template <typename T>
+void sweep_reverse(ggp_graph* h, T* vb, const T* vbar, T* xg, hipStream_t st) {
+    const Graph& g = h->g;
+    tstart(h, TM_SWEEP_REV, st);
+    for (size_t b = g.offsets.size() - 1; b >= 1; --b) {
+        if (g.offsets[b] > g.offsets[b - 1])
+            launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), g.offsets[b - 1],
+                                g.offsets[b], st);
+    }
+    if (g.n0 > 0) launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), 0, g.n0, st);
+    tstop(h, TM_SWEEP_REV, st);
+}
+
+// Points past the last level are never refined by the reference (values stay zero).
+template <typename T>
+void zero_tail(ggp_graph* h, T* x, hipStream_t st) {
+    const int64_t end = h->g.offsets.back();
+    if (end < h->g.N) launch_fill<T>(x + end, T(0), h->g.N - end, st);
+}
+
+// ================================== ops ========================================================
+template <typename T>
+int op_generate(ggp_graph* h, const T* xi, T* out, hipStream_t user) {
+    if (int rc = check_ready(h)) return rc;
+    if (int rc = enter(h, user)) return rc;
+    Graph& g = h->g;
+    const Table<T>& tb = table<T>(h);
+    T *xt = tp<T>(h->xt), *v = tp<T>(h->v);
+    launch_gather<T>(xt, xi, g.idx, g.N, h->s_main);
+    if (int rc = fork(h)) return rc;
+    dense_factor_async<T>(h, h->s_side);
+    dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_side);
+    factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr, nullptr);
+    if (int rc = join(h)) return rc;
+    zero_tail<T>(h, v, h->s_main);
+    sweep_forward<T>(h, v, xt, g.n0, h->s_main);
+    launch_scatter<T>(out, v, g.idx, g.N, h->s_main);
+    if (int rc = finish(h, user)) return rc;
+    if (*h->hinfo != 0) {
+        if (int rc = dense_retry<T>(h)) return rc;
+        dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_main);
+        sweep_forward<T>(h, v, xt, g.n0, h->s_main);
+        launch_scatter<T>(out, v, g.idx, g.N, h->s_main);
+        HC(hipStreamSynchronize(h->s_main));
+    }
+    return 0;
+}
+
+template <typename T>
+int op_generate_inv(ggp_graph* h, const T* values, T* xi_out, hipStream_t user) {
+    if (int rc = check_ready(h)) return rc;
+    if (int rc = enter(h, user)) return rc;
+    Graph& g = h->g;
+    T *vt = tp<T>(h->v), *xt = tp<T>(h->xt);
+    launch_gather<T>(vt, values, g.idx, g.N, h->s_main);
+    if (int rc = fork(h)) return rc;
+    dense_factor_async<T>(h, h->s_side);
+    dense_trsv<T>(tp<T>(h->A), (int)g.n0, vt, xt, h->s_side);
+    factor_t<T>(h, F_INV, nullptr, nullptr, nullptr, nullptr, vt, xt + g.n0);
+    if (int rc = join(h)) return rc;
+    launch_scatter<T>(xi_out, xt, g.idx, g.N, h->s_main);
+    if (int rc = finish(h, user)) return rc;
+    if (*h->hinfo != 0) {
+        if (int rc = dense_retry<T>(h)) return rc;
+        dense_trsv<T>(tp<T>(h->A), (int)g.n0, vt, xt, h->s_main);
+        launch_scatter<T>(xi_out, xt, g.idx, g.N, h->s_main);
+        HC(hipStreamSynchronize(h->s_main));
+    }
+    return 0;
+}
+
+template <typename T>
+int op_logdet(ggp_graph* h, bool dense, double* out, hipStream_t user) {
+    if (int rc = check_ready(h)) return rc;
+    if (int rc = enter(h, user)) return rc;
+    Graph& g = h->g;
+    launch_fill<double>(h->dscal, 0.0, 8, h->s_main);
+    launch_fill<int>(h->info, 0, 1, h->s_main);
+    if (dense) {
+        if (int rc = fork(h)) return rc;
+        dense_factor_async<T>(h, h->s_side);
+        dense_logdiag<T>(tp<T>(h->A), (int)g.n0, h->dscal + 1, h->s_side);
+    }
+    if (g.M > 0) {
+        factor_t<T>(h, F_TERMS, nullptr, nullptr, nullptr, h->scal_partial, nullptr,
+                         nullptr);
+        launch_reduce_scalar(h->dscal, h->scal_partial, (int)h->nblk_factor, nullptr, h->s_main);
+    }
+    if (dense)
+        if (int rc = join(h)) return rc;
+    if (int rc = finish(h, user)) return rc;
+    if (dense && *h->hinfo != 0) {
+        if (int rc = dense_retry<T>(h)) return rc;
+        dense_logdiag<T>(tp<T>(h->A), (int)g.n0, h->dscal + 1, h->s_main);
+        HC(hipMemcpyAsync(h->hscal, h->dscal, 8 * sizeof(double), hipMemcpyDeviceToHost, h->s_main));
+        HC(hipStreamSynchronize(h->s_main));
+    }
+    *out = h->hscal[0] + (dense ? h->hscal[1] : 0.0);
+    return 0;
+}
+
+template <typename T>
+int op_refine_logdet_terms(ggp_graph* h, T* terms, hipStream_t user) {
+    if (int rc = check_ready(h)) return rc;
+    if (int rc = enter(h, user)) return rc;
+    if (h->g.M > 0)
+        factor_t<T>(h, F_TERMS, nullptr, nullptr, terms, h->scal_partial, nullptr,
+                         nullptr);
+    return finish(h, user);
+}
+
+template <typename T>
+int op_refine_inv(ggp_graph* h, const T* values, T* xi_ref, hipStream_t user) {
+    if (int rc = check_ready(h)) return rc;
+    if (int rc = enter(h, user)) return rc;
+    if (h->g.M > 0)
+        factor_t<T>(h, F_INV, nullptr, nullptr, nullptr, nullptr, values, xi_ref);
+    return finish(h, user);
+}
+
+template <typename T>
+int op_refine(ggp_graph* h, T* values, const T* xi_ref, hipStream_t user) {
+    if (int rc = check_ready(h)) return rc;
+    if (int rc = enter(h, user)) return rc;
+    if (h->g.M > 0) {
+        factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr,
+                         nullptr, nullptr);
+        sweep_forward<T>(h, values, xi_ref, 0, h->s_main);
+    }
+    return finish(h, user);
+}
+
+template <typename T>
+int op_grad_xi(ggp_graph* h, const T* vbar, T* xbar, hipStream_t user) {
+    if (int rc = check_ready(h)) return rc;
+    if (int rc = enter(h, user)) return rc;
+    Graph& g = h->g;
+    T *vbt = tp<T>(h->vbt), *vb = tp<T>(h->vb), *xg = tp<T>(h->xg);
+    launch_gather<T>(vbt, vbar, g.idx, g.N, h->s_main);
+    if (int rc = fork(h)) return rc;
+    dense_factor_async<T>(h, h->s_side);
+    factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr,
+                     nullptr);
+    zero_tail<T>(h, xg, h->s_main);
+    sweep_reverse<T>(h, vb, vbt, xg, h->s_main);
+    if (int rc = join(h)) return rc;
+    dense_trmv_t<T>(tp<T>(h->A), (int)g.n0, vb, xg, h->s_main);
+    launch_scatter<T>(xbar, xg, g.idx, g.N, h->s_main);
+    if (int rc = finish(h, user)) return rc;
+    if (*h->hinfo != 0) {
+        if (int rc = dense_retry<T>(h)) return rc;
+        dense_trmv_t<T>(tp<T>(h->A), (int)g.n0, vb, xg, h->s_main);
+        launch_scatter<T>(xbar, xg, g.idx, g.N, h->s_main);
+        HC(hipStreamSynchronize(h->s_main));
+    }
+    return 0;
+}
+
+// Dense-layer cotangent for the op, enqueued on `st` into the dense rows of h->hist.
+enum DenseGrad { DG_NONE, DG_LOGDET, DG_GENERATE, DG_INVLOSS };
+
+template <typename T>
+void dense_grad(ggp_graph* h, int kind, hipStream_t st) {
+    const Graph& g = h->g;
+    const Table<T>& tb = table<T>(h);
+    double* rows = h->hist + (size_t)h->nblk_pull * h->hist_nb;
+    const int n = (int)g.n0;
+    if (kind == DG_LOGDET) {
+        dense_logdiag<T>(tp<T>(h->A), n, h->dscal + 1, st);
+        dense_grad_logdet<T>(g, tb, tp<T>(h->A), h->W, h->C, rows, h->nw_dense, st);
+    } else if (kind == DG_GENERATE) {
+        dense_grad_generate<T>(g, tb, tp<T>(h->A), tp<T>(h->vb), tp<T>(h->xt), h->W, h->C, h->Q,
+                               h->u, rows, h->nw_dense, st);
+    } else if (kind == DG_INVLOSS) {
+        // xi_dense = L \ y, alpha = L^-T xi_dense (src/dense.jl:229-240).
+        T* xid = tp<T>(h->xt);
+        T* alpha = tp<T>(h->tmp);
+        dense_trsv<T>(tp<T>(h->A), n, tp<T>(h->v), xid, st);
+        dense_trsv_t<T>(tp<T>(h->A), n, xid, alpha, st);
+        launch_sumsq_half<T>(xid, n, h->dscal + 1, st);
+        dense_grad_invloss<T>(g, tb, alpha, rows, h->nw_dense, st);
+    }
+}
+
+// Shared driver of the four d/dvals ops.
+//   mode: P_LOGDET / P_INVLOSS / P_GENVALS pullback; dense: which dense cotangent to add.
+template <typename T>
+int op_grad_vals(ggp_graph* h, int mode, int dkind, const T* in1, const T* in2, T* d_vals,
+                 double* scalar_out, hipStream_t user) {
+    if (int rc = check_ready(h)) return rc;
+    if (dkind != DG_NONE)
+        if (int rc = ensure_dense64(h)) return rc;
+    if (int rc = enter(h, user)) return rc;
+    Graph& g = h->g;
+    const Table<T>& tb = table<T>(h);
+    const int nb = tb.P.nb;
+    T *v = tp<T>(h->v), *xt = tp<T>(h->xt), *vb = tp<T>(h->vb), *vbt = tp<T>(h->vbt);
+    launch_fill<double>(h->dscal, 0.0, 8, h->s_main);
+    launch_fill<int>(h->info, 0, 1, h->s_main);
+    const T* pull_v = nullptr;
+    if (mode == P_GENVALS) {  // generate_grad_vals: forward field, then the reverse sweep
+        launch_gather<T>(xt, in1, g.idx, g.N, h->s_main);
+        launch_gather<T>(vbt, in2, g.idx, g.N, h->s_main);
+        if (int rc = fork(h)) return rc;
+        dense_factor_async<T>(h, h->s_side);
+        dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_side);
+        factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr, nullptr);
+        if (int rc = join(h)) return rc;
+        zero_tail<T>(h, v, h->s_main);
+        sweep_forward<T>(h, v, xt, g.n0, h->s_main);
+        sweep_reverse<T>(h, vb, vbt, nullptr, h->s_main);
+        pull_v = v;
+        if (int rc = fork(h)) return rc;
+        dense_grad<T>(h, DG_GENERATE, h->s_side);
+    } else {
+        if (mode == P_INVLOSS) {  // inverse loss: values (tree order)
+            if (dkind == DG_INVLOSS) {
+                launch_gather<T>(v, in1, g.idx, g.N, h->s_main);
+                pull_v = v;
+            } else {
+                pull_v = in1;
+            }
+        }
+        if (dkind != DG_NONE) {
+            if (int rc = fork(h)) return rc;
+            dense_factor_async<T>(h, h->s_side);
+            dense_grad<T>(h, dkind, h->s_side);
+        }
+    }
+    if (g.M > 0)
+        pullback_t<T>(h, mode, pull_v, xt, vb);
+    else
+        launch_fill<double>(h->hist, 0.0, (int64_t)h->nblk_pull * nb, h->s_main);
+    if (mode != P_GENVALS && g.M > 0)
+        launch_reduce_scalar(h->dscal, h->scal_partial, (int)h->nblk_pull, nullptr, h->s_main);
+    if (dkind != DG_NONE)
+        if (int rc = join(h)) return rc;
+    const int rows = (int)h->nblk_pull + (dkind != DG_NONE ? h->nw_dense : 0);
+    launch_reduce_hist<T>(d_vals, h->hist, rows, nb, nullptr, h->s_main);
+    if (int rc = finish(h, user)) return rc;
+    if (dkind != DG_NONE && *h->hinfo != 0) {
+        if (int rc = dense_retry<T>(h)) return rc;
+        if (mode == P_GENVALS) {
+            dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_main);
+            sweep_forward<T>(h, v, xt, g.n0, h->s_main);
+            sweep_reverse<T>(h, vb, vbt, nullptr, h->s_main);
+            pullback_t<T>(h, mode, v, xt, vb);
+        }
+        dense_grad<T>(h, dkind, h->s_main);
+        launch_reduce_hist<T>(d_vals, h->hist, rows, nb, nullptr, h->s_main);
+        HC(hipMemcpyAsync(h->hscal, h->dscal, 8 * sizeof(double), hipMemcpyDeviceToHost, h->s_main));
+        HC(hipStreamSynchronize(h->s_main));
+    }
+    if (scalar_out) *scalar_out = h->hscal[0] + (dkind != DG_NONE ? h->hscal[1] : 0.0);
+    return 0;
+}
+
+// ---- graph creation -----------------------------------------------------------------------
+int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const int64_t* offs,
+           int64_t n_off, const int64_t* indices, int64_t n0, int64_t k, int64_t N, int32_t D,
+           double scale, int32_t dtype) {
+    if (!out) return fail(GGP_ERR_ARG, "null output handle");
+    *out = nullptr;
+    if (!supported_k(k)) return fail(GGP_ERR_K, "unsupported k (supported: 4, 8, 10, 16)");
+    if (!supported_d(D)) return fail(GGP_ERR_D, "unsupported D (supported: 2, 3, 4)");
+    if (dtype != GGP_F32 && dtype != GGP_F64) return fail(GGP_ERR_ARG, "dtype must be GGP_F32 or GGP_F64");
+    if (!(std::isfinite(scale) && scale > 0)) return fail(GGP_ERR_ARG, "scale must be finite and > 0");
+    if (N < 1 || n0 < 1 || n0 > N) return fail(GGP_ERR_GRAPH, "need 1 <= n0 <= N");
+    if (N > INT32_MAX) return fail(GGP_ERR_ARG, "N must fit in int32");
+    if (n0 > 16384) return fail(GGP_ERR_ARG, "n0 above 16384 is not supported");
+    const int64_t M = N - n0;
+    if ((uint64_t)M * (uint64_t)k >= (1ull << 32)) return fail(GGP_ERR_ARG, "M*k must be < 2^32");
+    if (!coords || (M > 0 && !nbrs) || !offs) return fail(GGP_ERR_ARG, "null input array");
+    // check_graph (src/graph_build.jl:20-57)
+    if (n_off < 1) return fail(GGP_ERR_GRAPH, "offsets is empty");
+    if (offs[0] != n0) return fail(GGP_ERR_GRAPH, "offsets[0] must equal n0");
+    for (int64_t b = 1; b < n_off; ++b)
+        if (offs[b] < offs[b - 1]) return fail(GGP_ERR_GRAPH, "offsets must be non-decreasing");
+    if (offs[n_off - 1] > N) return fail(GGP_ERR_GRAPH, "offsets[end] must be <= N");
+    {
+        int64_t b = 1;
+        for (int64_t m = 0; m < M; ++m) {
+            const int64_t p = n0 + m;
+            while (b < n_off && offs[b] <= p) ++b;
+            const int64_t prev_end = b < n_off ? offs[b - 1] : offs[n_off - 1];
+            for (int64_t j = 0; j < k; ++j) {
+                const int64_t q = nbrs[m * k + j];
+                if (q < 0 || q >= N) return fail(GGP_ERR_GRAPH, "neighbour index out of range");
+                if (q >= p) return fail(GGP_ERR_GRAPH, "neighbour does not precede its point (not topological)");
+                if (b < n_off && q >= prev_end)
+                    return fail(GGP_ERR_GRAPH, "neighbour in its own depth level; neighbours must be in earlier levels");
+            }
+        }
+    }
+    if (indices) {
+        std::vector<char> seen((size_t)N, 0);
+        for (int64_t i = 0; i < N; ++i) {
+            if (indices[i] < 0 || indices[i] >= N || seen[(size_t)indices[i]])
+                return fail(GGP_ERR_GRAPH, "indices must be a permutation of 0..N-1");
+            seen[(size_t)indices[i]] = 1;
+        }
+    }
+    for (int64_t i = 0; i < N * D; ++i)
+        if (coords[i] >= (1u << 25)) return fail(GGP_ERR_ARG, "lattice coordinates must be < 2^25");
+
+    ggp_graph* h = new ggp_graph();
+    auto bail = [&](int rc) { free_all(h); delete h; return rc; };
+    h->dtype = dtype;
+    if (hipGetDevice(&h->dev) != hipSuccess) return bail(fail(GGP_ERR_HIP, "no HIP device"));
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, h->dev) == hipSuccess) {
+        h->ncu = std::max(1, prop.multiProcessorCount);
+        h->lds_max = std::min<size_t>(prop.sharedMemPerBlock, 65536);
+    }
+    if (const char* e = std::getenv("GGP_FACTOR_BLOCKS_PER_CU")) h->nblk_factor = (unsigned)(h->ncu * std::max(1, atoi(e)));
+    else h->nblk_factor = (unsigned)(h->ncu * 4);
+    if (const char* e = std::getenv("GGP_PULL_BLOCKS_PER_CU")) h->nblk_pull = (unsigned)(h->ncu * std::max(1, atoi(e)));
+    else h->nblk_pull = (unsigned)(h->ncu * 2);
+    h->nblk_factor = (unsigned)std::max<int64_t>(1, std::min<int64_t>(h->nblk_factor, (M + kBlock - 1) / kBlock));
+    h->nblk_pull = (unsigned)std::max<int64_t>(1, std::min<int64_t>(h->nblk_pull, (M + kBlock - 1) / kBlock));
+    h->nw_dense = (int)std::max<int64_t>(1, std::min<int64_t>(h->ncu, (n0 * (n0 + 1) / 2 + kBlock - 1) / kBlock));
+    Graph& g = h->g;
+    g.N = N; g.n0 = n0; g.M = M; g.K = k; g.D = D; g.scale = scale;
+    g.offsets.assign(offs, offs + n_off);
+    const size_t es = dtype == GGP_F32 ? 4 : 8;
+    // neighbours: int32 structure of arrays
+    std::vector<int32_t> nsoa((size_t)(M * k));
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t j = 0; j < k; ++j) nsoa[(size_t)(j * M + m)] = (int32_t)nbrs[m * k + j];
+    // reverse neighbour list over the points that lie in a level, consumers by decreasing p
+    const int64_t mlev = std::max<int64_t>(0, offs[n_off - 1] - n0);
+    std::vector<int64_t> rptr((size_t)N + 1, 0);
+    for (int64_t m = 0; m < mlev; ++m)
+        for (int64_t j = 0; j < k; ++j) rptr[(size_t)nbrs[m * k + j] + 1]++;
+    for (int64_t q = 0; q < N; ++q) rptr[(size_t)q + 1] += rptr[(size_t)q];
+    std::vector<uint32_t> rev((size_t)std::max<int64_t>(rptr[(size_t)N], 1));
+    {
+        std::vector<int64_t> pos(rptr.begin(), rptr.end() - 1);
+        for (int64_t m = mlev - 1; m >= 0; --m)
+            for (int64_t j = 0; j < k; ++j) {
+                const int64_t q = nbrs[m * k + j];
+                rev[(size_t)pos[(size_t)q]++] = (uint32_t)(m * k + j);
+            }
+    }
+    std::vector<int32_t> idx32;
+    if (indices) {
+        idx32.resize((size_t)N);
+        for (int64_t i = 0; i < N; ++i) idx32[(size_t)i] = (int32_t)indices[i];
+    }
+    int rc = 0;
+    rc |= dmalloc(h, (void**)&g.coords, (size_t)(N * D) * 4);
+    rc |= dmalloc(h, (void**)&g.nbr, nsoa.size() * 4);
+    rc |= dmalloc(h, (void**)&g.rev_ptr, rptr.size() * 8);
+    rc |= dmalloc(h, (void**)&g.rev, rev.size() * 4);
+    if (indices) rc |= dmalloc(h, (void**)&g.idx, (size_t)N * 4);
+    rc |= dmalloc(h, &h->mv, (size_t)(M * k) * es);
+    rc |= dmalloc(h, &h->sd, (size_t)M * es);
+    rc |= dmalloc(h, &h->v, (size_t)N * es);
+    rc |= dmalloc(h, &h->xt, (size_t)N * es);
+    rc |= dmalloc(h, &h->vb, (size_t)N * es);
+    rc |= dmalloc(h, &h->vbt, (size_t)N * es);
+    rc |= dmalloc(h, &h->xg, (size_t)N * es);
+    rc |= dmalloc(h, &h->tmp, (size_t)n0 * es);
+    rc |= dmalloc(h, &h->A, (size_t)(n0 * n0) * es);
+    rc |= dmalloc(h, (void**)&h->scal_partial, std::max(h->nblk_factor, h->nblk_pull) * 8);
+    rc |= dmalloc(h, (void**)&h->dscal, 8 * 8);
+    rc |= dmalloc(h, (void**)&h->info, 16);
+    if (rc) return bail(GGP_ERR_HIP);
+    if (hipHostMalloc((void**)&h->hscal, 8 * 8) != hipSuccess ||
+        hipHostMalloc((void**)&h->hinfo, 16) != hipSuccess)
+        return bail(fail(GGP_ERR_HIP, "hipHostMalloc failed"));
+    if (hipMemcpy(g.coords, coords, (size_t)(N * D) * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(g.nbr, nsoa.data(), nsoa.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(g.rev_ptr, rptr.data(), rptr.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(g.rev, rev.data(), rev.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        (indices && hipMemcpy(g.idx, idx32.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess))
+        return bail(fail(GGP_ERR_HIP, "hipMemcpy of the graph failed"));
+    if (hipStreamCreateWithFlags(&h->s_main, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&h->s_side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&h->ev_fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&h->ev_join, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&h->ev_user, hipEventDisableTiming) != hipSuccess)
+        return bail(fail(GGP_ERR_HIP, "stream/event creation failed"));
+    *out = h;
+    return 0;
+}
+
+}  // namespace
+
+// ================================== C ABI ======================================================
+#define DISPATCH(h, CALL_F, CALL_D) ((h)->dtype == GGP_F32 ? (CALL_F) : (CALL_D))
+
+extern "C" {
+
+const char* ggp_last_error(void) { return g_last_error.c_str(); }
+
+int ggp_supported(int64_t k, int32_t D) {
+    if (!supported_k(k)) return fail(GGP_ERR_K, "unsupported k");
+    if (!supported_d(D)) return fail(GGP_ERR_D, "unsupported D");
+    return 0;
+}
+
+int ggp_graph_create(ggp_graph** out, const uint32_t* coords_host, const int64_t* neighbors_host,
+                     const int64_t* offsets_host, int64_t n_offsets, const int64_t* indices_host,
+                     int64_t n0, int64_t k, int64_t N, int32_t D, double scale, int32_t dtype) {
+    return create(out, coords_host, neighbors_host, offsets_host, n_offsets, indices_host, n0, k,
+                  N, D, scale, dtype);
+}
+
+int ggp_graph_destroy(ggp_graph* h) {
+    if (!h) return 0;
+    (void)hipSetDevice(h->dev);
+    if (h->s_main) (void)hipStreamSynchronize(h->s_main);
+    if (h->s_side) (void)hipStreamSynchronize(h->s_side);
+    free_all(h);
+    delete h;
+    return 0;
+}
+
+int ggp_graph_shape(const ggp_graph* h, int64_t* N, int64_t* n0, int64_t* k, int32_t* D,
+                    int64_t* n_levels, int32_t* dtype) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    if (N) *N = h->g.N;
+    if (n0) *n0 = h->g.n0;
+    if (k) *k = h->g.K;
+    if (D) *D = h->g.D;
+    if (n_levels) *n_levels = (int64_t)h->g.offsets.size() - 1;
+    if (dtype) *dtype = h->dtype;
+    return 0;
+}
+
+int ggp_kernel_timers(ggp_graph* h, int32_t enable) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    (void)hipSetDevice(h->dev);
+    if (enable && !h->tev[0])
+        for (int i = 0; i < 2 * TM_COUNT; ++i)
+            if (hipEventCreate(&h->tev[i]) != hipSuccess) return fail(GGP_ERR_HIP, "hipEventCreate failed");
+    h->timing = enable != 0;
+    for (int t = 0; t < TM_COUNT; ++t) { h->tms[t] = 0; h->tcnt[t] = 0; h->tpending[t] = false; }
+    return 0;
+}
+
+int ggp_kernel_timer_read(const ggp_graph* h, const char* name, double* total_ms, int64_t* count) {
+    if (!h || !name) return fail(GGP_ERR_ARG, "null argument");
+    for (int t = 0; t < TM_COUNT; ++t)
+        if (std::strcmp(name, kTimerNames[t]) == 0) {
+            if (total_ms) *total_ms = h->tms[t];
+            if (count) *count = h->tcnt[t];
+            return 0;
+        }
+    return fail(GGP_ERR_ARG, std::string("unknown timer ") + name);
+}
+
+int ggp_set_cov_iso(ggp_graph* h, const void* bins_host, const void* vals_host, int64_t nbins) {
+    if (!h || !bins_host || !vals_host) return fail(GGP_ERR_ARG, "null argument");
+    if (hipSetDevice(h->dev) != hipSuccess) return fail(GGP_ERR_HIP, "hipSetDevice failed");
+    return DISPATCH(h, set_cov<float>(h, (const float*)bins_host, (const float*)vals_host, nbins),
+                    set_cov<double>(h, (const double*)bins_host, (const double*)vals_host, nbins));
+}
+
+#define ST(s) ((hipStream_t)(s))
+
+int ggp_generate(ggp_graph* h, const void* xi, void* out, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_generate<float>(h, (const float*)xi, (float*)out, ST(stream)),
+                    op_generate<double>(h, (const double*)xi, (double*)out, ST(stream)));
+}
+int ggp_generate_inv(ggp_graph* h, const void* values, void* xi, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_generate_inv<float>(h, (const float*)values, (float*)xi, ST(stream)),
+                    op_generate_inv<double>(h, (const double*)values, (double*)xi, ST(stream)));
+}
+int ggp_generate_logdet(ggp_graph* h, double* out, void* stream) {
+    if (!h || !out) return fail(GGP_ERR_ARG, "null argument");
+    return DISPATCH(h, op_logdet<float>(h, true, out, ST(stream)),
+                    op_logdet<double>(h, true, out, ST(stream)));
+}
+int ggp_refine_logdet(ggp_graph* h, double* out, void* stream) {
+    if (!h || !out) return fail(GGP_ERR_ARG, "null argument");
+    return DISPATCH(h, op_logdet<float>(h, false, out, ST(stream)),
+                    op_logdet<double>(h, false, out, ST(stream)));
+}
+int ggp_refine_logdet_terms(ggp_graph* h, void* terms, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_refine_logdet_terms<float>(h, (float*)terms, ST(stream)),
+                    op_refine_logdet_terms<double>(h, (double*)terms, ST(stream)));
+}
+int ggp_refine_inv(ggp_graph* h, const void* values_tree, void* xi_ref, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_refine_inv<float>(h, (const float*)values_tree, (float*)xi_ref, ST(stream)),
+                    op_refine_inv<double>(h, (const double*)values_tree, (double*)xi_ref, ST(stream)));
+}
+int ggp_refine(ggp_graph* h, void* values_tree, const void* xi_ref, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_refine<float>(h, (float*)values_tree, (const float*)xi_ref, ST(stream)),
+                    op_refine<double>(h, (double*)values_tree, (const double*)xi_ref, ST(stream)));
+}
+int ggp_generate_grad_xi(ggp_graph* h, const void* vbar, void* xbar, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_grad_xi<float>(h, (const float*)vbar, (float*)xbar, ST(stream)),
+                    op_grad_xi<double>(h, (const double*)vbar, (double*)xbar, ST(stream)));
+}
+int ggp_generate_grad_vals(ggp_graph* h, const void* xi, const void* vbar, void* d_vals,
+                           void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_grad_vals<float>(h, P_GENVALS, DG_GENERATE, (const float*)xi, (const float*)vbar, (float*)d_vals, nullptr, ST(stream)),
+                    op_grad_vals<double>(h, P_GENVALS, DG_GENERATE, (const double*)xi, (const double*)vbar, (double*)d_vals, nullptr, ST(stream)));
+}
+int ggp_refine_logdet_grad_vals(ggp_graph* h, void* d_vals, double* logdet, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_grad_vals<float>(h, P_LOGDET, DG_NONE, nullptr, nullptr, (float*)d_vals, logdet, ST(stream)),
+                    op_grad_vals<double>(h, P_LOGDET, DG_NONE, nullptr, nullptr, (double*)d_vals, logdet, ST(stream)));
+}
+int ggp_generate_logdet_grad_vals(ggp_graph* h, void* d_vals, double* logdet, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_grad_vals<float>(h, P_LOGDET, DG_LOGDET, nullptr, nullptr, (float*)d_vals, logdet, ST(stream)),
+                    op_grad_vals<double>(h, P_LOGDET, DG_LOGDET, nullptr, nullptr, (double*)d_vals, logdet, ST(stream)));
+}
+int ggp_refine_inv_loss_grad_vals(ggp_graph* h, const void* values_tree, void* d_vals,
+                                  double* loss, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_grad_vals<float>(h, P_INVLOSS, DG_NONE, (const float*)values_tree, nullptr, (float*)d_vals, loss, ST(stream)),
+                    op_grad_vals<double>(h, P_INVLOSS, DG_NONE, (const double*)values_tree, nullptr, (double*)d_vals, loss, ST(stream)));
+}
+int ggp_generate_inv_loss_grad_vals(ggp_graph* h, const void* data, void* d_vals, double* loss,
+                                    void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_grad_vals<float>(h, P_INVLOSS, DG_INVLOSS, (const float*)data, nullptr, (float*)d_vals, loss, ST(stream)),
+                    op_grad_vals<double>(h, P_INVLOSS, DG_INVLOSS, (const double*)data, nullptr, (double*)d_vals, loss, ST(stream)));
+}
+
+}  // extern "C"

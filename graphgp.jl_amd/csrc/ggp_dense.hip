@@ -1,0 +1,512 @@
+// ggp_dense.hip — the dense first layer (n0 x n0) on the GPU: src/dense.jl and the dense parts
+// of src/grad.jl / src/grad_generate_vals.jl, which the reference runs on the host every call.
+//
+// Factor and solves (precision T) accumulate every entry as the same fma chain, in the same
+// order, as the unblocked column-by-column Cholesky / substitution: a right-looking blocked
+// update that folds each 32-wide panel into the trailing entries in column order produces
+// exactly the left-looking sums. Gradients (f64 internally) use the matrix form of the
+// Cholesky adjoint, Abar = L^-T Phi(L^T Lbar) L^-1 (Phi = lower triangle, halved diagonal),
+// instead of the reference's scalar reverse sweep (src/grad_generate_vals.jl:18-39), which is
+// the same derivative evaluated in a parallel order.
+#include "ggp_internal.h"
+
+namespace ggp {
+
+__device__ inline float bcast(float x, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+__device__ inline double bcast(double x, int lane) {
+    const long long v = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_readlane((int)(v & 0xffffffffLL), lane);
+    const int hi = __builtin_amdgcn_readlane((int)(v >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+static inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+
+// ---- assembly (src/dense.jl:15-40) ----------------------------------------------------------
+template <typename T, int D>
+__global__ void k_dense_assemble(T* __restrict__ A, const uint32_t* __restrict__ coords, int n,
+                                 T scale, const TabEnt<T>* __restrict__ tab,
+                                 const uint16_t* __restrict__ acc, const TabParams<T>* __restrict__ Pp, T diag_add) {
+    const TabParams<T> P = *Pp;
+    const int j = blockIdx.x * 16 + threadIdx.x;
+    const int i = blockIdx.y * 16 + threadIdx.y;
+    if (i >= n || j > i) return;
+    if (i == j) {
+        A[(int64_t)i * n + i] = diag_add == T(0) ? P.v0 : P.v0 + diag_add;
+        return;
+    }
+    uint32_t ci[D], cj[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) { ci[d] = coords[(int64_t)i * D + d]; cj[d] = coords[(int64_t)j * D + d]; }
+    const T v = cov_lookup(radius<T>(sqdist<D>(ci, cj), scale), tab, acc, P);
+    A[(int64_t)i * n + j] = v;
+    A[(int64_t)j * n + i] = v;
+}
+
+// ---- blocked Cholesky -------------------------------------------------------------------------
+// Panel step kb: every workgroup (one wave) factors the diagonal tile in registers — lane r owns
+// row r, pivots are broadcast with readlane — then workgroup 1+t solves panel tile kb+1+t
+// against it. Workgroup 0 writes the diagonal tile and raises *info on a non-positive pivot
+// (LAPACK potrf's failure condition, src/dense.jl:47-48).
+template <typename T>
+__global__ void __launch_bounds__(64) k_potrf_panel(T* __restrict__ A, int n, int kb,
+                                                    int* __restrict__ info) {
+    __shared__ T sL[kTile][kTile + 1];
+    const int lane = threadIdx.x;
+    const int k0 = kb * kTile;
+    const int nk = min(kTile, n - k0);
+    T a[kTile];
+#pragma unroll
+    for (int c = 0; c < kTile; ++c)
+        a[c] = (lane < nk && c < nk && c <= lane) ? A[(int64_t)(k0 + lane) * n + k0 + c] : T(0);
+    bool bad = false;
+#pragma unroll
+    for (int jj = 0; jj < kTile; ++jj) {
+        if (jj < nk) {
+            const T piv = bcast(a[jj], jj);
+            bad = bad || !(piv > T(0));
+            const T d = num<T>::sqrt(piv);
+            const T l = a[jj] / d;
+            if (lane == jj) a[jj] = d;
+            else if (lane > jj) a[jj] = l;
+#pragma unroll
+            for (int c = jj + 1; c < kTile; ++c) {
+                if (c < nk) {
+                    const T lc = bcast(a[jj], c);
+                    if (c <= lane) a[c] = num<T>::fma(-a[jj], lc, a[c]);
+                }
+            }
+        }
+    }
+    if (lane < nk) {
+#pragma unroll
+        for (int c = 0; c < kTile; ++c)
+            if (c <= lane) sL[lane][c] = a[c];
+    }
+    if (blockIdx.x == 0) {
+        if (lane < nk) {
+#pragma unroll
+            for (int c = 0; c < kTile; ++c)
+                if (c <= lane && c < nk) A[(int64_t)(k0 + lane) * n + k0 + c] = a[c];
+        }
+        if (lane == 0 && bad) atomicOr(info, 1);
+        return;
+    }
+    __syncthreads();
+    const int r0 = (kb + (int)blockIdx.x) * kTile;
+    const int nr = min(kTile, n - r0);
+    if (lane >= nr) return;
+    T b[kTile];
+    T* row = A + (int64_t)(r0 + lane) * n + k0;
+#pragma unroll
+    for (int c = 0; c < kTile; ++c) b[c] = c < nk ? row[c] : T(0);
+#pragma unroll
+    for (int jj = 0; jj < kTile; ++jj) {
+        if (jj < nk) {
+            const T l = b[jj] / sL[jj][jj];
+            b[jj] = l;
+#pragma unroll
+            for (int c = jj + 1; c < kTile; ++c)
+                if (c < nk) b[c] = num<T>::fma(-l, sL[c][jj], b[c]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < kTile; ++c)
+        if (c < nk) row[c] = b[c];
+}
+
+// Trailing update after panel kb: tile (ib, jb), kb < jb <= ib, gets
+// a = fma(-L[i][p], L[j][p], a) for the panel columns p in order.
+template <typename T>
+__global__ void __launch_bounds__(256) k_potrf_update(T* __restrict__ A, int n, int kb) {
+    __shared__ T Pi[kTile][kTile + 1];
+    __shared__ T Pj[kTile][kTile + 1];
+    const int t = blockIdx.x;
+    int ti = (int)((sqrt(8.0 * t + 1.0) - 1.0) * 0.5);
+    while ((ti + 1) * (ti + 2) / 2 <= t) ++ti;
+    while (ti * (ti + 1) / 2 > t) --ti;
+    const int tj = t - ti * (ti + 1) / 2;
+    const int ib = kb + 1 + ti, jb = kb + 1 + tj;
+    const int k0 = kb * kTile, nk = min(kTile, n - k0);
+    const int i0 = ib * kTile, j0 = jb * kTile;
+    const int ni = min(kTile, n - i0), nj = min(kTile, n - j0);
+    for (int e = threadIdx.x; e < kTile * kTile; e += blockDim.x) {
+        const int r = e / kTile, c = e % kTile;
+        Pi[r][c] = (r < ni && c < nk) ? A[(int64_t)(i0 + r) * n + k0 + c] : T(0);
+        Pj[r][c] = (r < nj && c < nk) ? A[(int64_t)(j0 + r) * n + k0 + c] : T(0);
+    }
+    __syncthreads();
+    const int tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;
+    for (int r = ty; r < ni; r += blockDim.x / kTile) {
+        const int c = tx;
+        if (c >= nj || (ib == jb && c > r)) continue;
+        T* p = A + (int64_t)(i0 + r) * n + j0 + c;
+        T v = *p;
+        for (int q = 0; q < nk; ++q) v = num<T>::fma(-Pi[r][q], Pj[c][q], v);
+        *p = v;
+    }
+}
+
+template <typename T>
+void dense_potrf(T* A, int n, int* info, hipStream_t st) {
+    const int nt = (n + kTile - 1) / kTile;
+    for (int kb = 0; kb < nt; ++kb) {
+        hipLaunchKernelGGL((k_potrf_panel<T>), dim3(nt - kb), dim3(64), 0, st, A, n, kb, info);
+        const int m = nt - kb - 1;
+        if (m > 0)
+            hipLaunchKernelGGL((k_potrf_update<T>), dim3(m * (m + 1) / 2), dim3(256), 0, st, A, n, kb);
+    }
+}
+
+// ---- triangular products and solves ---------------------------------------------------------
+// y = L x (src/dense.jl:118): row i accumulates j = 0..i.
+template <typename T>
+__global__ void k_trmv(const T* __restrict__ L, int n, const T* __restrict__ x, T* __restrict__ y) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const T* row = L + (int64_t)i * n;
+    T acc = T(0);
+    for (int j = 0; j <= i; ++j) acc = num<T>::fma(row[j], x[j], acc);
+    y[i] = acc;
+}
+// y = L^T x (src/grad.jl:457, 493): entry i accumulates j = i..n-1.
+template <typename T>
+__global__ void k_trmv_t(const T* __restrict__ L, int n, const T* __restrict__ x, T* __restrict__ y) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    T acc = T(0);
+    for (int j = i; j < n; ++j) acc = num<T>::fma(L[(int64_t)j * n + i], x[j], acc);
+    y[i] = acc;
+}
+
+// x = L \ b (src/dense.jl:134), one workgroup: 32-row diagonal blocks solved by wave 0 with
+// broadcasts, the rows below updated by all threads; per entry the same fma chain as the
+// row-by-row substitution.
+template <typename T>
+__global__ void __launch_bounds__(256) k_trsv(const T* __restrict__ L, int n,
+                                              const T* __restrict__ b, T* __restrict__ x) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = b[i];
+    __syncthreads();
+    for (int k0 = 0; k0 < n; k0 += kTile) {
+        const int nk = min(kTile, n - k0);
+        if (threadIdx.x < 64) {
+            const int lane = threadIdx.x;
+            T v = lane < nk ? x[k0 + lane] : T(0);
+            for (int jj = 0; jj < nk; ++jj) {
+                const T xj = bcast(v, jj) / L[(int64_t)(k0 + jj) * n + k0 + jj];
+                if (lane == jj) v = xj;
+                else if (lane > jj && lane < nk)
+                    v = num<T>::fma(-L[(int64_t)(k0 + lane) * n + k0 + jj], xj, v);
+            }
+            if (lane < nk) x[k0 + lane] = v;
+        }
+        __syncthreads();
+        for (int i = k0 + nk + threadIdx.x; i < n; i += blockDim.x) {
+            T s = x[i];
+            const T* row = L + (int64_t)i * n + k0;
+            for (int p = 0; p < nk; ++p) s = num<T>::fma(-row[p], x[k0 + p], s);
+            x[i] = s;
+        }
+        __syncthreads();
+    }
+}
+
+// x = L^T \ b (src/dense.jl:236), blocked backward substitution.
+template <typename T>
+__global__ void __launch_bounds__(256) k_trsv_t(const T* __restrict__ L, int n,
+                                                const T* __restrict__ b, T* __restrict__ x) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = b[i];
+    __syncthreads();
+    const int nt = (n + kTile - 1) / kTile;
+    for (int kb = nt - 1; kb >= 0; --kb) {
+        const int k0 = kb * kTile, nk = min(kTile, n - k0);
+        if (threadIdx.x < 64) {
+            const int lane = threadIdx.x;
+            T v = lane < nk ? x[k0 + lane] : T(0);
+            for (int jj = nk - 1; jj >= 0; --jj) {
+                const T xj = bcast(v, jj) / L[(int64_t)(k0 + jj) * n + k0 + jj];
+                if (lane == jj) v = xj;
+                else if (lane < jj) v = num<T>::fma(-L[(int64_t)(k0 + jj) * n + k0 + lane], xj, v);
+            }
+            if (lane < nk) x[k0 + lane] = v;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < k0; i += blockDim.x) {
+            T s = x[i];
+            for (int p = 0; p < nk; ++p) s = num<T>::fma(-L[(int64_t)(k0 + p) * n + i], x[k0 + p], s);
+            x[i] = s;
+        }
+        __syncthreads();
+    }
+}
+
+// out = sum_i log L[i][i] (src/dense.jl:146), accumulated in double.
+template <typename T>
+__global__ void k_logdiag(const T* __restrict__ L, int n, double* __restrict__ out) {
+    __shared__ double s[256];
+    double t = 0.0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) t += (double)num<T>::log(L[(int64_t)i * n + i]);
+    s[threadIdx.x] = t;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) s[threadIdx.x] += s[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[0] = s[0];
+}
+
+template <typename T>
+void dense_trmv(const T* L, int n, const T* x, T* y, hipStream_t st) {
+    hipLaunchKernelGGL((k_trmv<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, L, n, x, y);
+}
+template <typename T>
+void dense_trmv_t(const T* L, int n, const T* x, T* y, hipStream_t st) {
+    hipLaunchKernelGGL((k_trmv_t<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, L, n, x, y);
+}
+template <typename T>
+void dense_trsv(const T* L, int n, const T* b, T* x, hipStream_t st) {
+    hipLaunchKernelGGL((k_trsv<T>), dim3(1), dim3(256), 0, st, L, n, b, x);
+}
+template <typename T>
+void dense_trsv_t(const T* L, int n, const T* b, T* x, hipStream_t st) {
+    hipLaunchKernelGGL((k_trsv_t<T>), dim3(1), dim3(256), 0, st, L, n, b, x);
+}
+template <typename T>
+void dense_logdiag(const T* L, int n, double* out, hipStream_t st) {
+    hipLaunchKernelGGL((k_logdiag<T>), dim3(1), dim3(256), 0, st, L, n, out);
+}
+
+template <typename T>
+void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStream_t st) {
+    const int n = (int)g.n0;
+    const dim3 grid(cdiv(n, 16), cdiv(n, 16)), blk(16, 16);
+    const T scale = (T)g.scale;
+    switch (g.D) {
+        case 2: hipLaunchKernelGGL((k_dense_assemble<T, 2>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add); break;
+        case 3: hipLaunchKernelGGL((k_dense_assemble<T, 3>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add); break;
+        case 4: hipLaunchKernelGGL((k_dense_assemble<T, 4>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add); break;
+        default: break;
+    }
+}
+
+// ---- dense cotangents (f64) -----------------------------------------------------------------
+// W = L^-1, one wave per column c: forward substitution of e_c with the column in LDS.
+// Lt64 is L^T in double (row i of Lt64 = column i of L), so the column reads are contiguous.
+template <typename T>
+__global__ void k_transpose64(const T* __restrict__ L, int n, double* __restrict__ Lt) {
+    const int j = blockIdx.x * 16 + threadIdx.x, i = blockIdx.y * 16 + threadIdx.y;
+    if (i < n && j < n) Lt[(int64_t)j * n + i] = j <= i ? (double)L[(int64_t)i * n + j] : 0.0;
+}
+
+__global__ void __launch_bounds__(64) k_trinv(const double* __restrict__ Lt, int n,
+                                              double* __restrict__ W) {
+    extern __shared__ double sx[];
+    const int c = blockIdx.x, lane = threadIdx.x;
+    for (int r = lane; r < n; r += 64) sx[r] = r == c ? 1.0 : 0.0;
+    __syncthreads();
+    for (int i = c; i < n; ++i) {
+        const double* col = Lt + (int64_t)i * n;
+        const double xi = sx[i] / col[i];
+        __syncthreads();
+        if (lane == 0) sx[i] = xi;
+        for (int r = i + 1 + lane; r < n; r += 64) sx[r] = __builtin_fma(-col[r], xi, sx[r]);
+        __syncthreads();
+    }
+    for (int r = lane; r < n; r += 64) W[(int64_t)r * n + c] = sx[r];
+}
+
+// C[i][j] = sum_{a >= max(i, j)} W[a][i] X[a][j] for lower-triangular W, X (n x n, row-major).
+// lower_only: only tiles with i >= j.
+__global__ void __launch_bounds__(256) k_wtx(const double* __restrict__ W,
+                                             const double* __restrict__ X, int n,
+                                             double* __restrict__ C, int lower_only) {
+    __shared__ double sW[kTile][kTile + 1];
+    __shared__ double sX[kTile][kTile + 1];
+    const int bi = blockIdx.y, bj = blockIdx.x;
+    if (lower_only && bj > bi) return;
+    const int i0 = bi * kTile, j0 = bj * kTile;
+    const int tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;
+    double acc[kTile / 8];
+#pragma unroll
+    for (int u = 0; u < kTile / 8; ++u) acc[u] = 0.0;
+    const int a_start = (max(i0, j0) / kTile) * kTile;
+    for (int a0 = a_start; a0 < n; a0 += kTile) {
+        for (int e = threadIdx.x; e < kTile * kTile; e += blockDim.x) {
+            const int r = e / kTile, c = e % kTile;
+            const int a = a0 + r;
+            sW[r][c] = (a < n && i0 + c < n) ? W[(int64_t)a * n + i0 + c] : 0.0;
+            sX[r][c] = (a < n && j0 + c < n) ? X[(int64_t)a * n + j0 + c] : 0.0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kTile / 8; ++u) {
+            const int ii = ty + 8 * u;
+#pragma unroll 8
+            for (int r = 0; r < kTile; ++r) acc[u] = __builtin_fma(sW[r][ii], sX[r][tx], acc[u]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < kTile / 8; ++u) {
+        const int i = i0 + ty + 8 * u, j = j0 + tx;
+        if (i < n && j < n) C[(int64_t)i * n + j] = acc[u];
+    }
+}
+
+// u = L^T vb (double), h/Q prefix pass: Q[a][j] = u[a] (sum_{j<=b<a} xi[b] W[b][j] + xi[a]W[a][j]/2)
+template <typename T>
+__global__ void k_ltv64(const T* __restrict__ L, int n, const T* __restrict__ vb,
+                        double* __restrict__ u) {
+    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= n) return;
+    double s = 0.0;
+    for (int i = a; i < n; ++i) s = __builtin_fma((double)L[(int64_t)i * n + a], (double)vb[i], s);
+    u[a] = s;
+}
+template <typename T>
+__global__ void k_qprefix(const double* __restrict__ W, int n, const T* __restrict__ xi,
+                          const double* __restrict__ u, double* __restrict__ Q) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    for (int a = 0; a < j; ++a) Q[(int64_t)a * n + j] = 0.0;
+    double h = 0.0;
+    for (int a = j; a < n; ++a) {
+        const double w = W[(int64_t)a * n + j] * (double)xi[a];
+        Q[(int64_t)a * n + j] = u[a] * (h + 0.5 * w);
+        h += w;
+    }
+}
+
+enum DenseMode { DM_LOGDET = 0, DM_GENERATE = 1, DM_INVLOSS = 2 };
+
+// Scatter the dense covariance cotangent through the lookup weights (src/dense.jl:166-181,
+// 244-252; src/grad_generate_vals.jl:196-211). Pairs (a >= b) of the lower triangle are split
+// over the grid; each workgroup accumulates an f64 LDS histogram and writes it to its row of
+// hist_partial.
+template <typename T, int D, int MODE>
+__global__ void __launch_bounds__(256) k_dense_scatter(const uint32_t* __restrict__ coords,
+                                                       int n, T scale,
+                                                       const TabEnt<T>* __restrict__ tab,
+                                                       const uint16_t* __restrict__ acc,
+                                                       const TabParams<T>* __restrict__ Pp,
+                                                       const double* __restrict__ C,
+                                                       const T* __restrict__ alpha,
+                                                       double* __restrict__ hist_partial) {
+    const TabParams<T> P = *Pp;
+    extern __shared__ double s_hist[];
+    for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
+    __syncthreads();
+    const int64_t npairs = (int64_t)n * (n + 1) / 2;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < npairs; t += stride) {
+        int64_t a = (int64_t)((sqrt(8.0 * (double)t + 1.0) - 1.0) * 0.5);
+        while ((a + 1) * (a + 2) / 2 <= t) ++a;
+        while (a * (a + 1) / 2 > t) --a;
+        const int64_t b = t - a * (a + 1) / 2;
+        double gv;
+        if (MODE == DM_LOGDET) {
+            const double kinv = C[a * n + b];
+            gv = a == b ? 0.5 * kinv : kinv;
+        } else if (MODE == DM_GENERATE) {
+            gv = a == b ? C[a * n + a] : C[a * n + b] + C[b * n + a];
+        } else {
+            const double aa = (double)alpha[a], ab = (double)alpha[b];
+            gv = a == b ? -0.5 * aa * aa : -aa * ab;
+        }
+        if (a == b) {
+            atomicAdd(&s_hist[0], gv);
+            continue;
+        }
+        uint32_t ca[D], cb[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) { ca[d] = coords[a * D + d]; cb[d] = coords[b * D + d]; }
+        const T r = radius<T>(sqdist<D>(ca, cb), scale);
+        T wlo, whi;
+        const int lo = cov_weights(r, tab, acc, P, wlo, whi);
+        atomicAdd(&s_hist[lo], gv * (double)wlo);
+        atomicAdd(&s_hist[lo + 1], gv * (double)whi);
+    }
+    __syncthreads();
+    double* out = hist_partial + (size_t)blockIdx.x * P.nb;
+    for (int i = threadIdx.x; i < P.nb; i += blockDim.x) out[i] = s_hist[i];
+}
+
+template <typename T>
+size_t dense_scatter_lds(const Table<T>& tb) { return (size_t)tb.P.nb * sizeof(double); }
+
+template <typename T, int MODE>
+static void launch_dense_scatter(const Graph& g, const Table<T>& tb, const double* C,
+                                 const T* alpha, double* hist_partial, int nw, hipStream_t st) {
+    const size_t lds = dense_scatter_lds(tb);
+    const int n = (int)g.n0;
+    const T scale = (T)g.scale;
+    switch (g.D) {
+        case 2: hipLaunchKernelGGL((k_dense_scatter<T, 2, MODE>), dim3(nw), dim3(256), lds, st, g.coords, n, scale, tb.tab, tb.acc, tb.params, C, alpha, hist_partial); break;
+        case 3: hipLaunchKernelGGL((k_dense_scatter<T, 3, MODE>), dim3(nw), dim3(256), lds, st, g.coords, n, scale, tb.tab, tb.acc, tb.params, C, alpha, hist_partial); break;
+        case 4: hipLaunchKernelGGL((k_dense_scatter<T, 4, MODE>), dim3(nw), dim3(256), lds, st, g.coords, n, scale, tb.tab, tb.acc, tb.params, C, alpha, hist_partial); break;
+        default: break;
+    }
+}
+
+template <typename T>
+static void dense_inverse64(const T* L, int n, double* W, double* Lt, hipStream_t st) {
+    hipLaunchKernelGGL((k_transpose64<T>), dim3(cdiv(n, 16), cdiv(n, 16)), dim3(16, 16), 0, st, L, n, Lt);
+    hipLaunchKernelGGL(k_trinv, dim3(n), dim3(64), (size_t)n * sizeof(double), st, Lt, n, W);
+}
+
+// d(sum log diag L)/dvals: Kinv = W^T W, diagonal halved (src/dense.jl:153-183).
+template <typename T>
+void dense_grad_logdet(const Graph& g, const Table<T>& tb, const T* L, double* W, double* C,
+                       double* hist_partial, int nw, hipStream_t st) {
+    const int n = (int)g.n0;
+    dense_inverse64(L, n, W, C, st);  // C doubles as the L^T scratch
+    const dim3 grid(cdiv(n, kTile), cdiv(n, kTile));
+    hipLaunchKernelGGL(k_wtx, grid, dim3(256), 0, st, W, W, n, C, 1);
+    launch_dense_scatter<T, DM_LOGDET>(g, tb, C, nullptr, hist_partial, nw, st);
+}
+
+// d<vb, L xi>/dvals through the Cholesky adjoint with Lbar = tril(vb xi^T)
+// (src/grad_generate_vals.jl:188-211): S = W^T P W with P = Phi(L^T Lbar), P[a][b] = u[a]xi[b]
+// (a > b), u[a]xi[a]/2 (a = b), u = L^T vb; Abar[i][j] = S[i][j] + S[j][i], Abar[j][j] = S[j][j].
+template <typename T>
+void dense_grad_generate(const Graph& g, const Table<T>& tb, const T* L, const T* vb,
+                         const T* xi, double* W, double* C, double* Q, double* u,
+                         double* hist_partial, int nw, hipStream_t st) {
+    const int n = (int)g.n0;
+    dense_inverse64(L, n, W, C, st);
+    hipLaunchKernelGGL((k_ltv64<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, L, n, vb, u);
+    hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, W, n, xi, u, Q);
+    const dim3 grid(cdiv(n, kTile), cdiv(n, kTile));
+    hipLaunchKernelGGL(k_wtx, grid, dim3(256), 0, st, W, Q, n, C, 0);
+    launch_dense_scatter<T, DM_GENERATE>(g, tb, C, nullptr, hist_partial, nw, st);
+}
+
+// d(0.5 y^T K^-1 y)/dvals: -alpha_a alpha_b, diagonal -alpha_a^2/2 (src/dense.jl:244-252).
+template <typename T>
+void dense_grad_invloss(const Graph& g, const Table<T>& tb, const T* alpha, double* hist_partial,
+                        int nw, hipStream_t st) {
+    launch_dense_scatter<T, DM_INVLOSS>(g, tb, nullptr, alpha, hist_partial, nw, st);
+}
+
+#define GGP_DENSE_INST(T)                                                                      \
+    template void dense_assemble<T>(const Graph&, const Table<T>&, T*, T, hipStream_t);        \
+    template void dense_potrf<T>(T*, int, int*, hipStream_t);                                  \
+    template void dense_trmv<T>(const T*, int, const T*, T*, hipStream_t);                     \
+    template void dense_trmv_t<T>(const T*, int, const T*, T*, hipStream_t);                   \
+    template void dense_trsv<T>(const T*, int, const T*, T*, hipStream_t);                     \
+    template void dense_trsv_t<T>(const T*, int, const T*, T*, hipStream_t);                   \
+    template void dense_logdiag<T>(const T*, int, double*, hipStream_t);                       \
+    template void dense_grad_logdet<T>(const Graph&, const Table<T>&, const T*, double*,       \
+                                       double*, double*, int, hipStream_t);                    \
+    template void dense_grad_generate<T>(const Graph&, const Table<T>&, const T*, const T*,    \
+                                         const T*, double*, double*, double*, double*,         \
+                                         double*, int, hipStream_t);                           \
+    template void dense_grad_invloss<T>(const Graph&, const Table<T>&, const T*, double*, int, \
+                                        hipStream_t);                                          \
+    template size_t dense_scatter_lds<T>(const Table<T>&);
+GGP_DENSE_INST(float)
+GGP_DENSE_INST(double)
+
+}  // namespace ggp

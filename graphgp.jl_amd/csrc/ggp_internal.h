@@ -1,0 +1,126 @@
+// ggp_internal.h — shared declarations of libgraphgp_hip (not part of the public ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "ggp_point.h"
+
+namespace ggp {
+
+constexpr int kBlock = 256;    // threads per workgroup of the per-point kernels
+constexpr int kTile = 32;      // dense-layer tile edge
+
+// Device-resident graph (the reference's GraphGPProblem arrays after to_backend).
+struct Graph {
+    int64_t N = 0, n0 = 0, M = 0, K = 0;
+    int D = 0;
+    double scale = 0;
+    uint32_t* coords = nullptr;    // N*D point-major
+    int32_t* nbr = nullptr;        // K*M, nbr[j*M + m]
+    int32_t* idx = nullptr;        // N, indices[tree] = orig, or null (identity)
+    int64_t* rev_ptr = nullptr;    // N+1: consumers of point q are rev[rev_ptr[q] .. rev_ptr[q+1])
+    uint32_t* rev = nullptr;       // m*K + j of each consumer, by decreasing consumer position
+    std::vector<int64_t> offsets;  // host copy, offsets[0] = n0
+};
+
+// Device-resident covariance table prepared for O(1) segment lookup.
+template <typename T>
+struct Table {
+    TabEnt<T>* tab = nullptr;   // nb-1 entries
+    TabParams<T>* params = nullptr;  // device copy of P
+    uint16_t* acc = nullptr;    // ucells+1 entries
+    TabParams<T> P{};
+    std::vector<T> bins, vals;  // host copies
+};
+
+enum FactorMode { F_MV = 1, F_TERMS = 2, F_INV = 4 };
+enum PullMode { P_LOGDET = 0, P_INVLOSS = 1, P_GENVALS = 2 };
+
+// Launchers of the per-point kernels for one (T, K); defined in ggp_point_kernels.h and
+// instantiated per (T, K) by ggp_inst.hip.
+template <typename T, int K>
+struct PointK {
+    static void factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
+                       double* partial, const T* values, T* xi_out, unsigned nblk,
+                       hipStream_t st);
+    static void pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, const T* xi,
+                         const T* vb, double* hist_partial, double* scalar_partial,
+                         unsigned nblk, hipStream_t st);
+    static void sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
+                          const T* sd, int64_t m_lo, int64_t len, hipStream_t st);
+    static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
+                          int64_t q_lo, int64_t q_hi, hipStream_t st);
+};
+extern template struct PointK<float, 4>;
+extern template struct PointK<float, 8>;
+extern template struct PointK<float, 10>;
+extern template struct PointK<float, 16>;
+extern template struct PointK<double, 4>;
+extern template struct PointK<double, 8>;
+extern template struct PointK<double, 10>;
+extern template struct PointK<double, 16>;
+
+// Dispatch over k (ggp_kernels.hip).
+template <typename T>
+void launch_factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
+                   double* partial, const T* values, T* xi_out, unsigned nblk, hipStream_t st);
+template <typename T>
+void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, const T* xi,
+                     const T* vb, double* hist_partial, double* scalar_partial, unsigned nblk,
+                     hipStream_t st);
+template <typename T>
+void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
+                      const T* sd, int64_t m_lo, int64_t len, hipStream_t st);
+template <typename T>
+void launch_sumsq_half(const T* x, int64_t n, double* out, hipStream_t st);
+template <typename T>
+void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
+                      int64_t q_lo, int64_t q_hi, hipStream_t st);
+template <typename T>
+void launch_reduce_hist(T* d_out, const double* partial, int nw, int nb, const double* extra,
+                        hipStream_t st);
+void launch_reduce_scalar(double* out, const double* in, int n, const double* add,
+                          hipStream_t st);
+template <typename T>
+void launch_gather(T* out, const T* in, const int32_t* idx, int64_t n, hipStream_t st);
+template <typename T>
+void launch_scatter(T* out, const T* in, const int32_t* idx, int64_t n, hipStream_t st);
+template <typename T>
+void launch_fill(T* p, T v, int64_t n, hipStream_t st);
+template <typename T>
+void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st);
+
+// Dense first layer (ggp_dense.hip). Matrices are n x n row-major; L lower.
+template <typename T>
+void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStream_t st);
+template <typename T>
+void dense_potrf(T* A, int n, int* info, hipStream_t st);
+template <typename T>
+void dense_trmv(const T* L, int n, const T* x, T* y, hipStream_t st);
+template <typename T>
+void dense_trmv_t(const T* L, int n, const T* x, T* y, hipStream_t st);
+template <typename T>
+void dense_trsv(const T* L, int n, const T* b, T* x, hipStream_t st);
+template <typename T>
+void dense_trsv_t(const T* L, int n, const T* b, T* x, hipStream_t st);
+template <typename T>
+void dense_logdiag(const T* L, int n, double* out, hipStream_t st);
+// Dense cotangent pipelines (f64 internally). Each writes d/dvals of the dense term, accumulated
+// per workgroup into hist_partial[nw][nb]; returns nw through *nw_out.
+template <typename T>
+void dense_grad_logdet(const Graph& g, const Table<T>& tb, const T* L, double* W, double* C,
+                       double* hist_partial, int nw, hipStream_t st);
+template <typename T>
+void dense_grad_generate(const Graph& g, const Table<T>& tb, const T* L, const T* vb,
+                         const T* xi, double* W, double* C, double* Q, double* u,
+                         double* hist_partial, int nw, hipStream_t st);
+template <typename T>
+void dense_grad_invloss(const Graph& g, const Table<T>& tb, const T* alpha, double* hist_partial,
+                        int nw, hipStream_t st);
+template <typename T>
+size_t dense_scatter_lds(const Table<T>& tb);
+
+}  // namespace ggp

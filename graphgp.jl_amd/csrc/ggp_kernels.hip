@@ -1,0 +1,179 @@
+// ggp_kernels.hip — element-wise and reduction kernels, and the (k)-dispatch to the per-point
+// kernel instantiations (ggp_point_kernels.h, compiled per (T, k) from ggp_inst.hip).
+#include "ggp_internal.h"
+
+namespace ggp {
+
+// Block-wide double sum of one value per thread; result valid in thread 0.
+__device__ inline double block_sum_g(double v, double* s_red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o, 64);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    if (l == 0) s_red[w] = v;
+    __syncthreads();
+    double t = 0.0;
+    if (threadIdx.x == 0)
+        for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += s_red[i];
+    return t;
+}
+
+// d_out[i] = T(sum_w partial[w][i] + extra[i]); one thread per bin, fixed order over w.
+template <typename T>
+__global__ void k_reduce_hist(T* __restrict__ d_out, const double* __restrict__ partial, int nw,
+                              int nb, const double* __restrict__ extra) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nb) return;
+    double s = 0.0;
+    for (int w = 0; w < nw; ++w) s += partial[(size_t)w * nb + i];
+    if (extra) s += extra[i];
+    d_out[i] = (T)s;
+}
+
+// out[0] = sum of n doubles (single block, fixed order per thread then tree).
+__global__ void k_reduce_scalar(double* __restrict__ out, const double* __restrict__ in, int n,
+                                const double* __restrict__ add) {
+    __shared__ double s_red[kBlock / 64];
+    double t = 0.0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) t += in[i];
+    t = block_sum_g(t, s_red);
+    if (threadIdx.x == 0) out[0] = t + (add ? add[0] : 0.0);
+}
+
+// out[0] = sum_i x_i^2 / 2 in double (the dense part of the inverse loss, src/grad.jl:521).
+template <typename T>
+__global__ void k_sumsq_half(const T* __restrict__ x, int64_t n, double* __restrict__ out) {
+    __shared__ double s_red[kBlock / 64];
+    double t = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) t += (double)x[i] * (double)x[i];
+    t = block_sum_g(t, s_red);
+    if (threadIdx.x == 0) out[0] = 0.5 * t;
+}
+template <typename T>
+void launch_sumsq_half(const T* x, int64_t n, double* out, hipStream_t st) {
+    hipLaunchKernelGGL((k_sumsq_half<T>), dim3(1), dim3(kBlock), 0, st, x, n, out);
+}
+
+// ---- permutations (src/orchestrate.jl:24, 38) -----------------------------------------------
+template <typename T>
+__global__ void k_gather(T* __restrict__ out, const T* __restrict__ in,
+                         const int32_t* __restrict__ idx, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = idx ? in[idx[i]] : in[i];
+}
+template <typename T>
+__global__ void k_scatter(T* __restrict__ out, const T* __restrict__ in,
+                          const int32_t* __restrict__ idx, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        if (idx) out[idx[i]] = in[i]; else out[i] = in[i];
+    }
+}
+template <typename T>
+__global__ void k_fill(T* __restrict__ p, T v, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+template <typename T>
+__global__ void k_copy(T* __restrict__ dst, const T* __restrict__ src, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+// ================================ launchers ===================================================
+static inline unsigned grid_for(int64_t n, int block = kBlock) {
+    return (unsigned)((n + block - 1) / block);
+}
+
+#define GGP_FOR_K(CALL)                              \
+    do {                                             \
+        switch (g.K) {                               \
+            case 4: CALL(4); break;                  \
+            case 8: CALL(8); break;                  \
+            case 10: CALL(10); break;                \
+            case 16: CALL(16); break;                \
+            default: break;                          \
+        }                                            \
+    } while (0)
+
+template <typename T>
+void launch_factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
+                   double* partial, const T* values, T* xi_out, unsigned nblk, hipStream_t st) {
+#define CALLF(KK) PointK<T, KK>::factor(g, tb, mode, mv, sd, terms, partial, values, xi_out, nblk, st)
+    GGP_FOR_K(CALLF);
+#undef CALLF
+}
+
+template <typename T>
+void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, const T* xi,
+                     const T* vb, double* hist_partial, double* scalar_partial, unsigned nblk,
+                     hipStream_t st) {
+#define CALLP(KK) PointK<T, KK>::pullback(g, tb, mode, v, xi, vb, hist_partial, scalar_partial, nblk, st)
+    GGP_FOR_K(CALLP);
+#undef CALLP
+}
+
+template <typename T>
+void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
+                      const T* sd, int64_t m_lo, int64_t len, hipStream_t st) {
+#define CALLS(KK) PointK<T, KK>::sweep_fwd(g, v, xi, xi_off, mv, sd, m_lo, len, st)
+    GGP_FOR_K(CALLS);
+#undef CALLS
+}
+
+template <typename T>
+void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
+                      int64_t q_lo, int64_t q_hi, hipStream_t st) {
+#define CALLR(KK) PointK<T, KK>::sweep_rev(g, vb, vbar, xg, mv, sd, q_lo, q_hi, st)
+    GGP_FOR_K(CALLR);
+#undef CALLR
+}
+
+template <typename T>
+void launch_reduce_hist(T* d_out, const double* partial, int nw, int nb, const double* extra,
+                        hipStream_t st) {
+    hipLaunchKernelGGL((k_reduce_hist<T>), dim3(grid_for(nb)), dim3(kBlock), 0, st, d_out,
+                       partial, nw, nb, extra);
+}
+
+void launch_reduce_scalar(double* out, const double* in, int n, const double* add,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(k_reduce_scalar, dim3(1), dim3(kBlock), 0, st, out, in, n, add);
+}
+
+template <typename T>
+void launch_gather(T* out, const T* in, const int32_t* idx, int64_t n, hipStream_t st) {
+    if (n > 0) hipLaunchKernelGGL((k_gather<T>), dim3(grid_for(n)), dim3(kBlock), 0, st, out, in, idx, n);
+}
+template <typename T>
+void launch_scatter(T* out, const T* in, const int32_t* idx, int64_t n, hipStream_t st) {
+    if (n > 0) hipLaunchKernelGGL((k_scatter<T>), dim3(grid_for(n)), dim3(kBlock), 0, st, out, in, idx, n);
+}
+template <typename T>
+void launch_fill(T* p, T v, int64_t n, hipStream_t st) {
+    if (n > 0) hipLaunchKernelGGL((k_fill<T>), dim3(grid_for(n)), dim3(kBlock), 0, st, p, v, n);
+}
+template <typename T>
+void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st) {
+    if (n > 0) hipLaunchKernelGGL((k_copy<T>), dim3(grid_for(n)), dim3(kBlock), 0, st, dst, src, n);
+}
+
+#define GGP_INST(T)                                                                            \
+    template void launch_factor<T>(const Graph&, const Table<T>&, int, T*, T*, T*, double*,    \
+                                   const T*, T*, unsigned, hipStream_t);                       \
+    template void launch_pullback<T>(const Graph&, const Table<T>&, int, const T*, const T*,   \
+                                     const T*, double*, double*, unsigned, hipStream_t);       \
+    template void launch_sweep_fwd<T>(const Graph&, T*, const T*, int64_t, const T*, const T*, \
+                                      int64_t, int64_t, hipStream_t);                          \
+    template void launch_sweep_rev<T>(const Graph&, T*, const T*, T*, const T*, const T*,      \
+                                      int64_t, int64_t, hipStream_t);                          \
+    template void launch_reduce_hist<T>(T*, const double*, int, int, const double*,            \
+                                        hipStream_t);                                          \
+    template void launch_gather<T>(T*, const T*, const int32_t*, int64_t, hipStream_t);        \
+    template void launch_scatter<T>(T*, const T*, const int32_t*, int64_t, hipStream_t);       \
+    template void launch_fill<T>(T*, T, int64_t, hipStream_t);                                 \
+    template void launch_sumsq_half<T>(const T*, int64_t, double*, hipStream_t);               \
+    template void launch_copy<T>(T*, const T*, int64_t, hipStream_t);
+GGP_INST(float)
+GGP_INST(double)
+template void launch_fill<int>(int*, int, int64_t, hipStream_t);
+
+}  // namespace ggp

@@ -1,0 +1,239 @@
+// ggp_point.h — per-point device primitives of the Vecchia refinement, for gfx950.
+//
+// One lane owns one refined point. The (k+1)x(k+1) covariance block, its Cholesky factor and
+// (in the adjoints) the factor/covariance cotangents live in VGPRs as packed lower triangles;
+// every loop over the block is unrolled at compile time (K, D are template parameters), so no
+// private array is ever indexed at run time and nothing goes to scratch for k <= 10.
+//
+// Arithmetic follows the reference expression by expression (file:line cited per function):
+// a multiply feeding an add/sub is a single fma exactly where the reference evaluates it under
+// @fastmath, and a separate multiply and add everywhere else. The library is compiled with
+// -ffp-contract=off, so the compiler fuses nothing by itself; division and square root are the
+// correctly rounded IEEE operations (HIP's defaults for f32 and f64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ggp {
+
+template <typename T> struct num;
+template <> struct num<float> {
+    using bits_t = uint32_t;
+    using sbits_t = int32_t;
+    __device__ __host__ static constexpr float eps() { return 1.1920928955078125e-7f; }
+    __device__ static inline float fma(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+    __device__ static inline float sqrt(float a) { return __builtin_sqrtf(a); }
+    __device__ static inline float log(float a) { return ::logf(a); }
+    __device__ static inline bits_t bits(float a) { return __float_as_uint(a); }
+};
+template <> struct num<double> {
+    using bits_t = uint64_t;
+    using sbits_t = int64_t;
+    __device__ __host__ static constexpr double eps() { return 2.220446049250313e-16; }
+    __device__ static inline double fma(double a, double b, double c) { return __builtin_fma(a, b, c); }
+    __device__ static inline double sqrt(double a) { return __builtin_sqrt(a); }
+    __device__ static inline double log(double a) { return ::log(a); }
+    __device__ static inline bits_t bits(double a) { return (bits_t)__double_as_longlong(a); }
+};
+
+// Index of (i, j), i >= j, in a packed lower triangle.
+__host__ __device__ constexpr int tri(int i, int j) { return i * (i + 1) / 2 + j; }
+
+// ---- covariance table -------------------------------------------------------------------------
+// Entry `lo` of the interpolation table: the bracketing segment [bins[lo], bins[lo+1]).
+// `slope` is (vals[lo+1]-vals[lo]) / (bins[lo+1]-bins[lo]) evaluated once in T, which is the
+// same IEEE value the reference computes inline (src/interp.jl:30).
+template <typename T> struct __attribute__((aligned(4 * sizeof(T)))) TabEnt {
+    T x0, y0, slope, x1;
+};
+
+// Scalars that describe the table and its O(1) segment index.
+//
+// The reference finds `lo` (bins[lo] <= r < bins[lo+1]) by binary search (src/interp.jl:17-27).
+// Here the segment is found from the IEEE bit pattern of r, which is monotone in r for r >= 0:
+// cell c = (bits(r) - bits(bins[1])) >> shift, and acc[c+1] is the largest lo with bins[lo] <=
+// the smallest value of cell c. Starting there and stepping forward while bins[lo+1] <= r gives
+// the unique lo with bins[lo] <= r < bins[lo+1] — the binary search's answer — for any strictly
+// increasing table; on log-spaced tables the forward step runs at most about once.
+template <typename T> struct TabParams {
+    T b0, b1, bl, v0, vl;          // bins[0], bins[1], bins[nb-1], vals[0], vals[nb-1]
+    typename num<T>::bits_t base;  // bits(bins[1])
+    int shift;                     // cell width in ulps = 2^shift
+    int ucells;                    // number of cells U; acc has U+1 entries
+    int nb;                        // number of bins
+};
+
+template <typename T>
+__device__ inline int seg_index(T r, const TabEnt<T>* __restrict__ tab,
+                                const uint16_t* __restrict__ acc, const TabParams<T>& P) {
+    using S = typename num<T>::sbits_t;
+    S d = (S)(num<T>::bits(r) - P.base);
+    int cell = d < 0 ? 0 : (int)min((S)(d >> P.shift) + 1, (S)P.ucells);
+    int lo = acc[cell];
+    while (r >= tab[lo].x1) ++lo;  // bounded: bins[nb-1] > r here
+    return lo;
+}
+
+// cov_lookup (src/interp.jl:10-34).
+template <typename T>
+__device__ inline T cov_lookup(T r, const TabEnt<T>* __restrict__ tab,
+                               const uint16_t* __restrict__ acc, const TabParams<T>& P) {
+    if (r <= P.b0) return P.v0;
+    if (r >= P.bl) return P.vl;
+    const TabEnt<T> e = tab[seg_index(r, tab, acc, P)];
+    return num<T>::fma(e.slope, r - e.x0, e.y0);  // @fastmath y0 + slope*(r - x0)
+}
+
+// cov_lookup_weights (src/interp.jl:62-83): value = wlo*vals[lo] + whi*vals[lo+1].
+template <typename T>
+__device__ inline int cov_weights(T r, const TabEnt<T>* __restrict__ tab,
+                                  const uint16_t* __restrict__ acc, const TabParams<T>& P,
+                                  T& wlo, T& whi) {
+    if (r <= P.b0) { wlo = T(1); whi = T(0); return 0; }
+    if (r >= P.bl) { wlo = T(0); whi = T(1); return P.nb - 2; }
+    const int lo = seg_index(r, tab, acc, P);
+    const TabEnt<T> e = tab[lo];
+    const T t = (r - e.x0) / (e.x1 - e.x0);
+    wlo = T(1) - t;
+    whi = t;
+    return lo;
+}
+
+// Exact squared lattice distance. The reference accumulates Int64 (src/linalg.jl:19-23); the
+// coordinates are < 2^21, so every term and the sum (< 2^46) are exact in double, and the
+// conversion to T below rounds the same integer once, as T(sq) does.
+template <int D>
+__device__ inline double sqdist(const uint32_t (&a)[D], const uint32_t (&b)[D]) {
+    double s = 0.0;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const double x = (double)((int32_t)a[d] - (int32_t)b[d]);
+        s = __builtin_fma(x, x, s);  // exact: all operands and results are integers < 2^53
+    }
+    return s;
+}
+
+// r = sqrt(T(sq)) * scale (src/linalg.jl:24; src/kernels_adjoint.jl:34).
+template <typename T>
+__device__ inline T radius(double sq, T scale) {
+    return num<T>::sqrt((T)sq) * scale;
+}
+
+// ---- the per-point block ------------------------------------------------------------------
+template <typename T, int K, int D>
+struct Block {
+    static constexpr int N = K + 1;
+    static constexpr int NT = N * (N + 1) / 2;
+    uint32_t jc[N][D];  // joint lattice coords: rows 0..K-1 the neighbours, row K the point
+    T A[NT];            // covariance, then its Cholesky factor (packed lower)
+
+    // _gather_joint! (src/kernels.jl:9-23). nbr is the int32 structure-of-arrays neighbour
+    // table nbr[j*M + m]; coords is point-major.
+    __device__ inline void gather(const uint32_t* __restrict__ coords,
+                                  const int32_t* __restrict__ nbr, int64_t M, int64_t m,
+                                  int64_t n0, int32_t (&nb)[K]) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) nb[j] = nbr[(int64_t)j * M + m];
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const uint32_t* c = coords + (int64_t)nb[j] * D;
+#pragma unroll
+            for (int d = 0; d < D; ++d) jc[j][d] = c[d];
+        }
+        const uint32_t* c = coords + (n0 + m) * D;
+#pragma unroll
+        for (int d = 0; d < D; ++d) jc[K][d] = c[d];
+    }
+
+    // assemble_cov! (src/linalg.jl:15-29).
+    __device__ inline void assemble(T scale, const TabEnt<T>* __restrict__ tab,
+                                    const uint16_t* __restrict__ acc, const TabParams<T>& P) {
+#pragma unroll
+        for (int a = 0; a < N; ++a) {
+            A[tri(a, a)] = P.v0;  // cov_lookup(0) = vals[1] since bins[1] = 0 <= 0
+#pragma unroll
+            for (int b = 0; b < a; ++b)
+                A[tri(a, b)] = cov_lookup(radius<T>(sqdist<D>(jc[a], jc[b]), scale), tab, acc, P);
+        }
+    }
+
+    // chol_lower! (src/linalg.jl:38-73), whole loop under @fastmath. The clamp branch is
+    // evaluated as a select so the wave never diverges; both arms produce the reference's
+    // values bit for bit.
+    __device__ inline void cholesky() {
+        const T pivmin = num<T>::eps() * A[0];
+        const T dmin = num<T>::sqrt(pivmin);
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            T s = A[tri(j, j)];
+#pragma unroll
+            for (int p = 0; p < j; ++p) s = num<T>::fma(-A[tri(j, p)], A[tri(j, p)], s);
+            const bool ok = s > pivmin;  // false for NaN, as in the reference
+            const T d = ok ? num<T>::sqrt(s) : dmin;
+            A[tri(j, j)] = d;
+#pragma unroll
+            for (int i = j + 1; i < N; ++i) {
+                T t = A[tri(i, j)];
+#pragma unroll
+                for (int p = 0; p < j; ++p) t = num<T>::fma(-A[tri(i, p)], A[tri(j, p)], t);
+                A[tri(i, j)] = ok ? t / d : T(0);
+            }
+        }
+    }
+
+    // mean_vec_solve! (src/linalg.jl:85-103), under @fastmath.
+    __device__ inline void mean_vec(T (&x)[K]) const {
+        const T pivfloor = T(1.5) * num<T>::sqrt(num<T>::eps()) * A[0];
+#pragma unroll
+        for (int i = K - 1; i >= 0; --i) {
+            const T d = A[tri(i, i)];
+            T s = A[tri(K, i)];
+#pragma unroll
+            for (int j = i + 1; j < K; ++j) s = num<T>::fma(-A[tri(j, i)], x[j], s);
+            x[i] = d > pivfloor ? s / d : T(0);
+        }
+    }
+
+    __device__ inline T stddev() const { return A[tri(K, K)]; }
+};
+
+// chol_pullback! (src/linalg.jl:112-137), under @fastmath. Lbar holds the factor cotangents on
+// entry and is consumed; Abar receives d/dA for the lower triangle.
+template <typename T, int N>
+__device__ inline void chol_pullback(T (&Abar)[N * (N + 1) / 2], T (&Lbar)[N * (N + 1) / 2],
+                                     const T (&L)[N * (N + 1) / 2]) {
+#pragma unroll
+    for (int j = N - 1; j >= 0; --j) {
+        const T ljj = L[tri(j, j)];
+#pragma unroll
+        for (int i = N - 1; i >= j + 1; --i) {
+            const T lbij = Lbar[tri(i, j)];
+            const T tbar = lbij / ljj;
+            Lbar[tri(j, j)] -= lbij * L[tri(i, j)] / ljj;
+            Abar[tri(i, j)] = tbar;
+#pragma unroll
+            for (int p = 0; p < j; ++p) {
+                Lbar[tri(i, p)] = num<T>::fma(-tbar, L[tri(j, p)], Lbar[tri(i, p)]);
+                Lbar[tri(j, p)] = num<T>::fma(-tbar, L[tri(i, p)], Lbar[tri(j, p)]);
+            }
+        }
+        const T sbar = Lbar[tri(j, j)] / (T(2) * ljj);
+        Abar[tri(j, j)] = sbar;
+#pragma unroll
+        for (int p = 0; p < j; ++p)
+            Lbar[tri(j, p)] = num<T>::fma(-(T(2) * sbar), L[tri(j, p)], Lbar[tri(j, p)]);
+    }
+}
+
+// ---- LDS staging of the table -----------------------------------------------------------
+// Cooperative copy of the prepared table (entries + cell index) from global memory into LDS.
+template <typename T>
+__device__ inline void stage_table(TabEnt<T>* s_tab, uint16_t* s_acc,
+                                   const TabEnt<T>* __restrict__ g_tab,
+                                   const uint16_t* __restrict__ g_acc, const TabParams<T>& P) {
+    for (int i = threadIdx.x; i < P.nb - 1; i += blockDim.x) s_tab[i] = g_tab[i];
+    for (int i = threadIdx.x; i <= P.ucells; i += blockDim.x) s_acc[i] = g_acc[i];
+    __syncthreads();
+}
+
+}  // namespace ggp

@@ -1,0 +1,143 @@
+/* graphgp_hip.h — C ABI of libgraphgp_hip, the MI355X (gfx950) implementation of GraphGP.jl's
+ * fused per-point Vecchia refinement.
+ *
+ * Conventions (those of the reference's accelerator ABI, csrc/graphgp_capi.cu:70-119):
+ *   - every function returns an int status, 0 = success; ggp_last_error() gives the message;
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream);
+ *   - arrays passed to the ops are DEVICE pointers of the problem's element type (float for
+ *     GGP_F32, double for GGP_F64) unless the name says _host;
+ *   - indices into points are 0-based.
+ * Status codes: 2 = k unsupported, 3 = D unsupported (as csrc/graphgp_capi.cu:53-68),
+ *   4 = malformed graph (the invariants of check_graph, src/graph_build.jl:20-57),
+ *   5 = HIP runtime error, 6 = dense first-layer covariance not positive definite even with
+ *   1e-2 relative jitter (src/dense.jl:65-66), 7 = invalid argument, 8 = no covariance set.
+ *
+ * The problem handle stands for the reference's GraphGPProblem after to_backend
+ * (src/types.jl:22-106): the handle owns device copies of the graph in the layout the kernels
+ * want (neighbours as int32 structure-of-arrays, a reverse neighbour list, the level table) and
+ * never retains caller buffers. One handle must not be used from two host threads at once;
+ * different handles are independent.
+ *
+ * All ops take and return arrays in the ORIGINAL point order, as src/orchestrate.jl does
+ * (xi[indices] gathered on input, out[indices] = values scattered on output); the refine_* ops
+ * work in tree order, as src/api.jl does. Every op returns after its work on `stream` is done.
+ */
+#ifndef GRAPHGP_HIP_H
+#define GRAPHGP_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ggp_graph ggp_graph;
+
+enum { GGP_F32 = 0, GGP_F64 = 1 };
+
+enum {
+    GGP_OK = 0,
+    GGP_ERR_K = 2,
+    GGP_ERR_D = 3,
+    GGP_ERR_GRAPH = 4,
+    GGP_ERR_HIP = 5,
+    GGP_ERR_NOT_PD = 6,
+    GGP_ERR_ARG = 7,
+    GGP_ERR_NO_COV = 8
+};
+
+/* Message for the last non-zero status returned on this host thread. */
+const char* ggp_last_error(void);
+
+/* Supported neighbour counts k and dimensions D (k in {4, 8, 10, 16}, D in {2, 3, 4}). */
+int ggp_supported(int64_t k, int32_t D);
+
+/* Problem construction = GraphGPProblem(coords, neighbors, offsets, n0, scale, bins, vals,
+ * indices) followed by to_backend (src/types.jl:32-56, 99-106). Host inputs:
+ *   coords_host    N*D uint32, point-major (the reference's (D,N) column-major lattice coords)
+ *   neighbors_host M*k int64, point-major (the reference's (K,M) column-major), 0-based,
+ *                  M = N - n0; every neighbour must lie in an earlier depth level
+ *   offsets_host   n_offsets int64, 0-based exclusive level ends, offsets[0] = n0,
+ *                  offsets[n_offsets-1] = N (the reference's `offsets`)
+ *   indices_host   N int64 or NULL; indices[tree_pos] = original_pos (the reference's `indices`)
+ *   scale          physical length of one lattice step (the reference's `scale`)
+ * The graph is validated as check_graph does (status 4 on a violation). */
+int ggp_graph_create(ggp_graph** out, const uint32_t* coords_host, const int64_t* neighbors_host,
+                     const int64_t* offsets_host, int64_t n_offsets, const int64_t* indices_host,
+                     int64_t n0, int64_t k, int64_t N, int32_t D, double scale, int32_t dtype);
+int ggp_graph_destroy(ggp_graph* h);
+
+/* Problem shape: N, n0, k, D, number of depth levels (excluding the dense level), dtype. */
+int ggp_graph_shape(const ggp_graph* h, int64_t* N, int64_t* n0, int64_t* k, int32_t* D,
+                    int64_t* n_levels, int32_t* dtype);
+
+/* Isotropic covariance table (bins, vals): the reference's prob.bins / prob.vals
+ * (src/types.jl:28-29; built by make_cov_bins / rbf_kernel / matern_kernel, src/extras.jl).
+ * Host arrays of the problem's element type; bins strictly increasing with bins[0] >= 0.
+ * Replacing the table is the analogue of _set_vals (src/chainrules.jl:18-21). */
+int ggp_set_cov_iso(ggp_graph* h, const void* bins_host, const void* vals_host, int64_t nbins);
+
+/* ---- forward ops -------------------------------------------------------------------------- */
+
+/* generate (src/orchestrate.jl:19-42): out = G(xi), both length N, original order. */
+int ggp_generate(ggp_graph* h, const void* xi, void* out, void* stream);
+
+/* generate_inv (src/orchestrate.jl:53-81): xi = G^-1(values), both length N, original order. */
+int ggp_generate_inv(ggp_graph* h, const void* values, void* xi, void* stream);
+
+/* generate_logdet (src/orchestrate.jl:89-97): dense + refinement log-determinant. */
+int ggp_generate_logdet(ggp_graph* h, double* logdet_host, void* stream);
+
+/* refine_logdet_terms (src/api.jl:30-57): terms[m] = log std_m, length M, tree order.
+ * refine_logdet (src/api.jl:24-27): the sum of those terms (accumulated in double). */
+int ggp_refine_logdet_terms(ggp_graph* h, void* terms, void* stream);
+int ggp_refine_logdet(ggp_graph* h, double* out_host, void* stream);
+
+/* refine_inv (src/api.jl:66-103): xi_ref[m] for the M refined points from values_tree (N). */
+int ggp_refine_inv(ggp_graph* h, const void* values_tree, void* xi_ref, void* stream);
+
+/* refine! (src/api.jl:113-141): values_tree (N, first n0 preset) is completed in place from
+ * xi_ref (M). */
+int ggp_refine(ggp_graph* h, void* values_tree, const void* xi_ref, void* stream);
+
+/* ---- adjoints ----------------------------------------------------------------------------- */
+
+/* generate_grad_xi (src/grad.jl:392-506): xbar = G^T vbar, both length N, original order. */
+int ggp_generate_grad_xi(ggp_graph* h, const void* vbar, void* xbar, void* stream);
+
+/* generate_grad_vals (src/grad_generate_vals.jl:111-282): d_vals (nbins) = d<vbar, G(xi)>/dvals.
+ * xi and vbar are length N, original order. */
+int ggp_generate_grad_vals(ggp_graph* h, const void* xi, const void* vbar, void* d_vals,
+                           void* stream);
+
+/* refine_logdet_grad_vals (src/grad.jl:96-119): d_vals = d(refine_logdet)/dvals; the logdet
+ * itself is written to *logdet_host when non-NULL (the fused form, src/grad.jl:680-715). */
+int ggp_refine_logdet_grad_vals(ggp_graph* h, void* d_vals, double* logdet_host, void* stream);
+
+/* generate_logdet_grad_vals (src/grad.jl:149-154) = generate_logdet_and_grad_vals
+ * (src/grad.jl:680-715): dense + refinement. */
+int ggp_generate_logdet_grad_vals(ggp_graph* h, void* d_vals, double* logdet_host, void* stream);
+
+/* refine_inv_loss_grad_vals (src/grad.jl:626-671): loss = 0.5*||refine_inv(values_tree)||^2 and
+ * its gradient w.r.t. vals. */
+int ggp_refine_inv_loss_grad_vals(ggp_graph* h, const void* values_tree, void* d_vals,
+                                  double* loss_host, void* stream);
+
+/* generate_inv_loss_grad_vals (src/grad.jl:514-529): 0.5*||generate_inv(data)||^2 and its
+ * gradient w.r.t. vals; data is length N, original order. */
+int ggp_generate_inv_loss_grad_vals(ggp_graph* h, const void* data, void* d_vals,
+                                    double* loss_host, void* stream);
+
+/* ---- measurement ------------------------------------------------------------------------- */
+/* No counterpart in the reference (its benchmarks time whole calls, bench/compare/run_julia.jl:50-58).
+ * When enabled, each op brackets its main kernels with HIP events on the stream they run on;
+ * ggp_kernel_timer_read returns the summed milliseconds and the number of timed launches for
+ * "factor", "pullback", "sweep_fwd", "sweep_rev", "dense" or "op" (whole op). Enabling resets. */
+int ggp_kernel_timers(ggp_graph* h, int32_t enable);
+int ggp_kernel_timer_read(const ggp_graph* h, const char* name, double* total_ms, int64_t* count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GRAPHGP_HIP_H */

@@ -1,0 +1,280 @@
+"""GPU parity: the HIP library through its C ABI against the oracle (CPU restatement of the
+reference) and against the reference's own golden fixtures.
+
+Tolerances are L2-norm relative (test/python_parity_generate.jl:26-36): 1e-5 for Float32 and
+1e-12 for Float64, the bar of this port; the fixture checks use the reference's own test
+tolerances (test/test_refine.jl, test/test_gradients.jl, test/python_parity_generate.jl).
+Forward ops are also checked for bit-exact agreement with the oracle: both evaluate the same
+IEEE operations in the same order.
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import load_fixture, relerr
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL, F64_TOL = 1e-5, 1e-12
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def G():
+    import graphgp_hip
+    return graphgp_hip
+
+
+def O():
+    import oracle
+    return oracle
+
+
+def fixture_problem(name, dtype):
+    z = load_fixture(name)
+    s = "64" if dtype == np.float64 else "32"
+    bins = z["cov_bins" + s] if "cov_bins" + s in z.files else z["cov_bins64"].astype(dtype)
+    vals = z["cov_vals" + s] if "cov_vals" + s in z.files else z["cov_vals64"].astype(dtype)
+    idx = z["indices"] if "indices" in z.files else None
+    prob = G().GraphGPProblem(z["coords"], z["neighbors"], z["offsets"], int(z["n0"]),
+                              float(z["scale"]), bins, vals, indices=idx)
+    ref = O().Problem(prob.coords, prob.neighbors, prob.offsets, prob.n0, prob.scale, prob.bins,
+                      prob.vals, indices=prob.indices, dtype=dtype)
+    return prob, ref, z
+
+
+def synth_problem(N, D, n0, k, dtype, seed=0, scale=0.1, nbins=500, jitter=1e-5):
+    rng = np.random.default_rng(seed)
+    pts = rng.random((N, D))
+    bins, vals = G().rbf_kernel(1.0, scale, 1e-4, 2.0, nbins, jitter=jitter)
+    prob = G().build_graph(pts, n0, k, bins.astype(dtype), vals.astype(dtype))
+    ref = O().Problem(prob.coords, prob.neighbors, prob.offsets, prob.n0, prob.scale, prob.bins,
+                      prob.vals, indices=prob.indices, dtype=dtype)
+    return prob, ref
+
+
+def tol(dtype):
+    return F32_TOL if dtype == np.float32 else F64_TOL
+
+
+DTYPES = [np.float32, np.float64]
+SYNTH = [(4000, 2, 100, 4), (4000, 3, 150, 8), (3000, 3, 120, 10), (3000, 3, 200, 16),
+         (3000, 4, 150, 8)]
+
+
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("name", ["small", "medium"])
+def test_refine_ops_vs_fixture_and_oracle(gpu, name, dtype):
+    _say(f"case refine_ops {name} {np.dtype(dtype).name}")
+    prob, ref, z = fixture_problem(name, dtype)
+    hp = G().to_backend(prob)
+    s = "64" if dtype == np.float64 else "32"
+    terms = G().refine_logdet_terms(hp)
+    ld = G().refine_logdet(hp)
+    xi = G().refine_inv(hp, z["values" + s])
+    v = G().refine(hp, z["initial_values" + s], z["xi_ref" + s])
+    # oracle
+    assert relerr(terms, ref.refine_logdet_terms()) < tol(dtype)
+    assert relerr(xi, ref.refine_inv(z["values" + s])) < tol(dtype)
+    assert relerr(v, ref.refine(z["initial_values" + s], z["xi_ref" + s])) < tol(dtype)
+    # reference fixtures at the reference's own tolerances (test/test_refine.jl:1-30)
+    if dtype == np.float64:
+        assert abs(ld - float(z["logdet64"])) <= 1e-6 * abs(float(z["logdet64"]))
+        np.testing.assert_allclose(xi, z["xi64"], rtol=1e-6, atol=1e-8)
+        np.testing.assert_allclose(v, z["refine_values64"], rtol=1e-6, atol=1e-8)
+    else:
+        assert abs(ld - float(z["logdet32"])) <= 2e-3 * abs(float(z["logdet32"]))
+        assert relerr(xi, z["xi32"]) < 1e-2
+        assert relerr(v, z["refine_values32"]) < 1e-2
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_refine_forward_bit_exact(gpu, dtype):
+    """Same IEEE operations in the same order as the oracle: identical bits."""
+    _say(f"case bit_exact {np.dtype(dtype).name}")
+    prob, ref, z = fixture_problem("small", dtype)
+    hp = G().to_backend(prob)
+    s = "64" if dtype == np.float64 else "32"
+    xi = G().refine_inv(hp, z["values" + s])
+    v = G().refine(hp, z["initial_values" + s], z["xi_ref" + s])
+    np.testing.assert_array_equal(xi, ref.refine_inv(z["values" + s]))
+    np.testing.assert_array_equal(v, ref.refine(z["initial_values" + s], z["xi_ref" + s]))
+
+
+def test_generate_parity_fixture(gpu):
+    """generate / generate_inv with a non-identity permutation, f64, <= 1e-12 L2
+    (test/python_parity_generate.jl)."""
+    _say("case generate_parity f64")
+    prob, ref, z = fixture_problem("generate_parity", np.float64)
+    hp = G().to_backend(prob)
+    f = G().generate(hp, z["xi"])
+    xi = G().generate_inv(hp, z["values"])
+    assert relerr(f, z["generate_field"]) < 1e-12
+    assert relerr(xi, z["generate_inv_xi"]) < 1e-12
+    assert relerr(G().generate_inv(hp, f), z["xi"]) < 1e-10
+    np.testing.assert_array_equal(f, ref.generate(z["xi"]))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_gradient_fixtures(gpu, dtype):
+    """d/dvals of logdet and of the inverse loss vs the JAX fixture (test/test_gradients.jl:1-26)."""
+    _say(f"case gradient_fixtures {np.dtype(dtype).name}")
+    prob, ref, z = fixture_problem("small", dtype)
+    hp = G().to_backend(prob)
+    s = "64" if dtype == np.float64 else "32"
+    g = G().refine_logdet_grad_vals(hp)
+    loss, gi = G().refine_inv_loss_grad_vals(hp, z["values" + s])
+    _, g_or = ref.refine_logdet_grad_vals()
+    loss_or, gi_or = ref.refine_inv_loss_grad_vals(z["values" + s])
+    assert relerr(g, g_or) < tol(dtype)
+    assert relerr(gi, gi_or) < tol(dtype)
+    assert abs(loss - loss_or) <= tol(dtype) * abs(loss_or)
+    if dtype == np.float64:
+        nz = z["grad_logdet_vals64"] != 0
+        np.testing.assert_allclose(g[nz], z["grad_logdet_vals64"][nz], rtol=1e-5, atol=1e-8)
+        assert abs(loss - float(z["inv_loss64"])) <= 1e-6 * float(z["inv_loss64"])
+        nz = z["grad_inv_loss_vals64"] != 0
+        np.testing.assert_allclose(gi[nz], z["grad_inv_loss_vals64"][nz], rtol=1e-4, atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", SYNTH, ids=lambda s: f"N{s[0]}_D{s[1]}_n0{s[2]}_k{s[3]}")
+def test_ops_vs_oracle(gpu, shape, dtype):
+    N, D, n0, k = shape
+    _say(f"case ops_vs_oracle N={N} D={D} n0={n0} k={k} {np.dtype(dtype).name}")
+    prob, ref = synth_problem(N, D, n0, k, dtype, seed=k * 10 + D)
+    hp = G().to_backend(prob)
+    rng = np.random.default_rng(1)
+    xi = rng.standard_normal(N).astype(dtype)
+    vb = rng.standard_normal(N).astype(dtype)
+    t = tol(dtype)
+    f = G().generate(hp, xi)
+    assert relerr(f, ref.generate(xi)) < t
+    assert relerr(G().generate_inv(hp, f), ref.generate_inv(f)) < t
+    assert abs(G().generate_logdet(hp) - ref.generate_logdet()) <= t * abs(ref.generate_logdet())
+    assert relerr(G().generate_grad_xi(hp, vb), ref.generate_grad_xi(vb)) < t
+    gv = G().generate_grad_vals(hp, xi, vb)
+    assert relerr(gv, ref.generate_grad_vals(xi, vb)) < (t if dtype == np.float32 else 1e-10)
+    ld, gl = G().generate_logdet_and_grad_vals(hp)
+    ld_o, gl_o = ref.generate_logdet_grad_vals()
+    assert abs(ld - ld_o) <= t * abs(ld_o)
+    assert relerr(gl, gl_o) < (t if dtype == np.float32 else 1e-10)
+    loss, gi = G().generate_inv_loss_grad_vals(hp, f)
+    loss_o, gi_o = ref.generate_inv_loss_grad_vals(f)
+    assert abs(loss - loss_o) <= t * abs(loss_o)
+    assert relerr(gi, gi_o) < (t if dtype == np.float32 else 1e-10)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_invariants(gpu, dtype):
+    """Round trip, adjoint identity, logdet = dense + refine (test/test_orchestrate.jl,
+    test/test_gradients.jl:56-77)."""
+    _say(f"case invariants {np.dtype(dtype).name}")
+    N, D, n0, k = 20000, 3, 300, 8
+    prob, ref = synth_problem(N, D, n0, k, dtype, seed=3, scale=0.05)
+    hp = G().to_backend(prob)
+    rng = np.random.default_rng(2)
+    xi = rng.standard_normal(N).astype(dtype)
+    vb = rng.standard_normal(N).astype(dtype)
+    f = G().generate(hp, xi)
+    back = G().generate_inv(hp, f)
+    assert relerr(back, xi) < (1e-3 if dtype == np.float32 else 1e-8)
+    gx = G().generate_grad_xi(hp, vb)
+    lhs = float(np.dot(vb.astype(float), f.astype(float)))
+    rhs = float(np.dot(gx.astype(float), xi.astype(float)))
+    assert abs(lhs - rhs) <= (1e-4 if dtype == np.float32 else 1e-10) * abs(lhs)
+    ld = G().generate_logdet(hp)
+    ldr = G().refine_logdet(hp)
+    L = ref.dense_factor()
+    ldd = float(np.sum(np.log(np.diag(L).astype(float))))
+    assert abs(ld - (ldd + ldr)) <= (1e-5 if dtype == np.float32 else 1e-12) * abs(ld)
+
+
+def test_generate_grad_vals_finite_differences(gpu):
+    """d<w, generate(vals)>/dvals vs central differences (test/test_grad_generate_vals.jl:5-33)."""
+    _say("case grad_vals_fd f64")
+    rng = np.random.default_rng(1)
+    N, D, n0, k = 2000, 3, 100, 8
+    pts = rng.standard_normal((N, D))
+    bins, vals = G().rbf_kernel(1.0, 0.3, 1e-4, 1e1, 50, jitter=1e-2)
+    prob = G().build_graph(pts, n0, k, bins, vals)
+    hp = G().to_backend(prob)
+    xi = rng.standard_normal(N)
+    w = rng.standard_normal(N)
+    dv = G().generate_grad_vals(hp, xi, w)
+    eps = 1e-6
+    for i in (5, 12, 25, 30, 40, 45):
+        e = np.zeros(len(vals))
+        e[i] = eps
+        fp = np.dot(w, G().generate(hp.set_vals(vals + e), xi))
+        fm = np.dot(w, G().generate(hp.set_vals(vals - e), xi))
+        fd = (fp - fm) / (2 * eps)
+        assert abs(dv[i] - fd) <= 1e-4 * abs(fd) + 1e-6, (i, dv[i], fd)
+    hp.set_vals(vals)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_dense_only_and_empty_levels(gpu, dtype):
+    """M = 0 (only the dense block) and a level list with an empty level."""
+    _say(f"case edge_shapes {np.dtype(dtype).name}")
+    prob, ref = synth_problem(600, 3, 60, 8, dtype, seed=9)
+    # empty level inserted after the first refined level
+    offs = np.concatenate([prob.offsets[:2], prob.offsets[1:2], prob.offsets[2:]])
+    p2 = G().GraphGPProblem(prob.coords, prob.neighbors, offs, prob.n0, prob.scale, prob.bins,
+                            prob.vals, indices=prob.indices)
+    r2 = O().Problem(p2.coords, p2.neighbors, p2.offsets, p2.n0, p2.scale, p2.bins, p2.vals,
+                     indices=p2.indices, dtype=dtype)
+    hp = G().to_backend(p2)
+    xi = np.random.default_rng(0).standard_normal(p2.N).astype(dtype)
+    assert relerr(G().generate(hp, xi), r2.generate(xi)) < tol(dtype)
+    assert relerr(G().generate_grad_xi(hp, xi), r2.generate_grad_xi(xi)) < tol(dtype)
+    # dense only
+    n = 80
+    p3 = G().GraphGPProblem(prob.coords[:n], np.zeros((0, 8), np.int64), np.array([n]), n,
+                            prob.scale, prob.bins, prob.vals)
+    r3 = O().Problem(p3.coords, p3.neighbors, p3.offsets, p3.n0, p3.scale, p3.bins, p3.vals,
+                     dtype=dtype)
+    hp3 = G().to_backend(p3)
+    x3 = xi[:n]
+    assert relerr(G().generate(hp3, x3), r3.generate(x3)) < tol(dtype)
+    assert abs(G().generate_logdet(hp3) - r3.generate_logdet()) <= tol(dtype) * abs(r3.generate_logdet())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_dense_jitter_retry(gpu, dtype):
+    """Coincident points make the dense block singular: the factorization is retried with
+    escalating jitter (src/dense.jl:46-67, test/test_dense.jl:54-62)."""
+    _say(f"case jitter_retry {np.dtype(dtype).name}")
+    prob, _ = synth_problem(800, 3, 80, 8, dtype, seed=11, jitter=0.0)
+    coords = prob.coords.copy()
+    coords[5] = coords[3]
+    coords[7] = coords[3]
+    p2 = G().GraphGPProblem(coords, prob.neighbors, prob.offsets, prob.n0, prob.scale,
+                            prob.bins, prob.vals, indices=prob.indices)
+    r2 = O().Problem(p2.coords, p2.neighbors, p2.offsets, p2.n0, p2.scale, p2.bins, p2.vals,
+                     indices=p2.indices, dtype=dtype)
+    hp = G().to_backend(p2)
+    xi = np.random.default_rng(4).standard_normal(p2.N).astype(dtype)
+    f = G().generate(hp, xi)
+    assert np.all(np.isfinite(f))
+    assert relerr(f, r2.generate(xi)) < (1e-4 if dtype == np.float32 else 1e-9)
+
+
+def test_op_without_table_and_bad_graph(gpu):
+    _say("case error_paths")
+    lib = __import__("graphgp_hip._native", fromlist=["hip"]).hip()
+    prob, _ = synth_problem(500, 3, 50, 8, np.float32, seed=2)
+    h = C.c_void_p()
+    rc = lib.ggp_graph_create(C.byref(h), prob.coords.ctypes.data, prob.neighbors.ctypes.data,
+                              prob.offsets.ctypes.data, len(prob.offsets), None, prob.n0, 8,
+                              prob.N, 3, prob.scale, 0)
+    assert rc == 0
+    out = C.c_double()
+    assert lib.ggp_generate_logdet(h, C.byref(out), None) == 8
+    assert lib.ggp_graph_destroy(h) == 0
