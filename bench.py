@@ -69,10 +69,17 @@ def cpu_baseline(prob, xi, vb, nthreads):
     import oracle as O
     ref = O.Problem(prob.coords, prob.neighbors, prob.offsets, prob.n0, prob.scale, prob.bins,
                     prob.vals, indices=prob.indices, dtype=np.float32, nthreads=nthreads)
+    ops = {"generate": lambda: ref.generate(xi), "grad_xi": lambda: ref.generate_grad_xi(vb),
+           "grad_vals": lambda: ref.generate_grad_vals(xi, vb)}
     t = {}
-    s = time.perf_counter(); ref.generate(xi); t["generate"] = time.perf_counter() - s
-    s = time.perf_counter(); ref.generate_grad_xi(vb); t["grad_xi"] = time.perf_counter() - s
-    s = time.perf_counter(); ref.generate_grad_vals(xi, vb); t["grad_vals"] = time.perf_counter() - s
+    for name, f in ops.items():   # one warm-up, then the best of three (whole op each)
+        f()
+        best = float("inf")
+        for _ in range(3):
+            s = time.perf_counter()
+            f()
+            best = min(best, time.perf_counter() - s)
+        t[name] = best
     return t
 
 
@@ -157,13 +164,15 @@ def main():
         "per_op": per_op, "kernels": kernels, "roofline": roofline,
     }
     if not args.no_cpu:
-        nthreads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+        # the host's CPU share: OMP_NUM_THREADS when the environment sets it, else the affinity
+        nthreads = int(os.environ.get("OMP_NUM_THREADS") or
+                       (len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
         log(f"cpu baseline on {nthreads} threads ...")
         t = cpu_baseline(prob, xi_np, vb_np, nthreads)
         tt = sum(t[o] for o in ("generate", "grad_xi", "grad_vals"))
         line["cpu_baseline"] = {
             "value": N / tt, "unit": "points/s", "cores": nthreads, "kind": "port",
-            "sample": "the full workload, one pass of each op (generate, grad_xi, grad_vals)",
+            "sample": "the full 1M-point workload; each op timed whole, best of 3 after a warm-up",
             "per_op_s": t, "speedup": (N / (total / args.steps)) / (N / tt)}
     print(json.dumps(line), flush=True)
 

@@ -341,9 +341,10 @@ void sweep_reverse(ggp_graph* h, T* vb, const T* vbar, T* xg, hipStream_t st) {
     for (size_t b = g.offsets.size() - 1; b >= 1; --b) {
         if (g.offsets[b] > g.offsets[b - 1])
             launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), g.offsets[b - 1],
-                                g.offsets[b], st);
+                                g.offsets[b], g.rev_group[b], st);
     }
-    if (g.n0 > 0) launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), 0, g.n0, st);
+    if (g.n0 > 0)
+        launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), 0, g.n0, g.rev_group[0], st);
     tstop(h, TM_SWEEP_REV, st);
 }
 
@@ -677,6 +678,16 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
                 const int64_t q = nbrs[m * k + j];
                 rev[(size_t)pos[(size_t)q]++] = (uint32_t)(m * k + j);
             }
+    }
+    // lanes per point of the reverse sweep: the power of two covering the level's largest fan-in
+    g.rev_group.assign((size_t)n_off, 1);
+    for (int64_t b = 0; b < n_off; ++b) {
+        const int64_t lo = b == 0 ? 0 : offs[b - 1], hi = b == 0 ? n0 : offs[b];
+        int64_t mx = 0;
+        for (int64_t q = lo; q < hi; ++q) mx = std::max(mx, rptr[(size_t)q + 1] - rptr[(size_t)q]);
+        int G = 1;
+        while (G < mx && G < 64) G <<= 1;
+        g.rev_group[(size_t)b] = G;
     }
     std::vector<int32_t> idx32;
     if (indices) {

@@ -46,75 +46,84 @@ __global__ void k_dense_assemble(T* __restrict__ A, const uint32_t* __restrict__
 }
 
 // ---- blocked Cholesky -------------------------------------------------------------------------
-// Panel step kb: every workgroup (one wave) factors the diagonal tile in registers — lane r owns
-// row r, pivots are broadcast with readlane — then workgroup 1+t solves panel tile kb+1+t
-// against it. Workgroup 0 writes the diagonal tile and raises *info on a non-positive pivot
-// (LAPACK potrf's failure condition, src/dense.jl:47-48).
-template <typename T>
-__global__ void __launch_bounds__(64) k_potrf_panel(T* __restrict__ A, int n, int kb,
-                                                    int* __restrict__ info) {
-    __shared__ T sL[kTile][kTile + 1];
-    const int lane = threadIdx.x;
+// Panel step kb (block column of kTile columns).
+//  1. Wave 0 of every workgroup factors the diagonal tile right-looking: lane r owns row r in
+//     registers; the pivot of column p comes from lane p by readlane, and the column's entries
+//     are broadcast through LDS (one wave: no block barrier, only a wave-level code-motion fence).
+//     Entry (r, c) receives fma(-L[r][p], L[c][p], .) for p = 0, 1, ... in order — the same fma
+//     chain as the left-looking recurrence. Workgroup 0 writes the tile back and raises *info on
+//     a non-positive pivot (LAPACK potrf's failure condition, src/dense.jl:47-48).
+//  2. After one block barrier every thread solves one row below the tile left-looking against
+//     the factored tile in LDS: (a_jj - sum_{p<jj} a_p L[jj][p]) / L[jj][jj].
+constexpr int kPanelThreads = 256;
+constexpr int kLStride = kTile + 4;  // LDS row stride: rows stay 16-byte aligned for b128 reads
+
+// FULL: the block column has all kTile columns (every panel but possibly the last), so the
+// loops carry no bounds checks.
+template <typename T, bool FULL>
+__global__ void __launch_bounds__(kPanelThreads) k_potrf_panel(T* __restrict__ A, int n, int kb,
+                                                               int* __restrict__ info) {
+    __shared__ __align__(16) T sL[kTile * kLStride];
+    __shared__ __align__(16) T scol[kTile];
+    const int tid = threadIdx.x;
     const int k0 = kb * kTile;
-    const int nk = min(kTile, n - k0);
-    T a[kTile];
+    const int nk = FULL ? kTile : min(kTile, n - k0);
+    if (tid < 64) {
+        // Entries above the diagonal are scratch: they receive harmless updates and are
+        // never read back, which keeps every update unconditional.
+        const int r = tid;
+        T a[kTile];
+        const T* rp = A + (int64_t)(k0 + (r < nk ? r : 0)) * n + k0;
 #pragma unroll
-    for (int c = 0; c < kTile; ++c)
-        a[c] = (lane < nk && c < nk && c <= lane) ? A[(int64_t)(k0 + lane) * n + k0 + c] : T(0);
-    bool bad = false;
+        for (int c = 0; c < kTile; ++c) a[c] = (r < nk && (FULL || c < nk)) ? rp[c] : T(0);
+        bool bad = false;
 #pragma unroll
-    for (int jj = 0; jj < kTile; ++jj) {
-        if (jj < nk) {
-            const T piv = bcast(a[jj], jj);
-            bad = bad || !(piv > T(0));
-            const T d = num<T>::sqrt(piv);
-            const T l = a[jj] / d;
-            if (lane == jj) a[jj] = d;
-            else if (lane > jj) a[jj] = l;
+        for (int p = 0; p < kTile; ++p) {
+            if (FULL || p < nk) {
+                const T piv = bcast(a[p], p);
+                bad = bad || !(piv > T(0));
+                const T d = num<T>::sqrt(piv);
+                const T l = a[p] / d;
+                a[p] = r == p ? d : l;
+                if (r < kTile) scol[r] = a[p];
+                __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int c = jj + 1; c < kTile; ++c) {
-                if (c < nk) {
-                    const T lc = bcast(a[jj], c);
-                    if (c <= lane) a[c] = num<T>::fma(-a[jj], lc, a[c]);
-                }
+                for (int c = p + 1; c < kTile; ++c) a[c] = num<T>::fma(-a[p], scol[c], a[c]);
+                __builtin_amdgcn_wave_barrier();
             }
         }
-    }
-    if (lane < nk) {
+        if (r < nk) {
 #pragma unroll
-        for (int c = 0; c < kTile; ++c)
-            if (c <= lane) sL[lane][c] = a[c];
-    }
-    if (blockIdx.x == 0) {
-        if (lane < nk) {
+            for (int c = 0; c < kTile; ++c) sL[r * kLStride + c] = a[c];
+            if (blockIdx.x == 0) {
+                T* wp = A + (int64_t)(k0 + r) * n + k0;
 #pragma unroll
-            for (int c = 0; c < kTile; ++c)
-                if (c <= lane && c < nk) A[(int64_t)(k0 + lane) * n + k0 + c] = a[c];
+                for (int c = 0; c < kTile; ++c)
+                    if (c <= r && (FULL || c < nk)) wp[c] = a[c];
+            }
         }
-        if (lane == 0 && bad) atomicOr(info, 1);
-        return;
+        if (blockIdx.x == 0 && r == 0 && bad) atomicOr(info, 1);
     }
     __syncthreads();
-    const int r0 = (kb + (int)blockIdx.x) * kTile;
-    const int nr = min(kTile, n - r0);
-    if (lane >= nr) return;
+    const int row = k0 + kTile + (int)blockIdx.x * kPanelThreads + tid;
+    if (row >= n) return;
     T b[kTile];
-    T* row = A + (int64_t)(r0 + lane) * n + k0;
+    T* rp = A + (int64_t)row * n + k0;
 #pragma unroll
-    for (int c = 0; c < kTile; ++c) b[c] = c < nk ? row[c] : T(0);
+    for (int c = 0; c < kTile; ++c) b[c] = (FULL || c < nk) ? rp[c] : T(0);
 #pragma unroll
     for (int jj = 0; jj < kTile; ++jj) {
-        if (jj < nk) {
-            const T l = b[jj] / sL[jj][jj];
-            b[jj] = l;
+        if (FULL || jj < nk) {
+            const T* lrow = sL + jj * kLStride;
+            T t = b[jj];
 #pragma unroll
-            for (int c = jj + 1; c < kTile; ++c)
-                if (c < nk) b[c] = num<T>::fma(-l, sL[c][jj], b[c]);
+            for (int p = 0; p < jj; ++p) t = num<T>::fma(-b[p], lrow[p], t);
+            b[jj] = t / lrow[jj];
         }
     }
 #pragma unroll
     for (int c = 0; c < kTile; ++c)
-        if (c < nk) row[c] = b[c];
+        if (FULL || c < nk) rp[c] = b[c];
 }
 
 // Trailing update after panel kb: tile (ib, jb), kb < jb <= ib, gets
@@ -153,7 +162,12 @@ template <typename T>
 void dense_potrf(T* A, int n, int* info, hipStream_t st) {
     const int nt = (n + kTile - 1) / kTile;
     for (int kb = 0; kb < nt; ++kb) {
-        hipLaunchKernelGGL((k_potrf_panel<T>), dim3(nt - kb), dim3(64), 0, st, A, n, kb, info);
+        const int below = n - kb * kTile - kTile;
+        const unsigned nblk = below > 0 ? (unsigned)((below + kPanelThreads - 1) / kPanelThreads) : 1u;
+        if (n - kb * kTile >= kTile)
+            hipLaunchKernelGGL((k_potrf_panel<T, true>), dim3(nblk), dim3(kPanelThreads), 0, st, A, n, kb, info);
+        else
+            hipLaunchKernelGGL((k_potrf_panel<T, false>), dim3(nblk), dim3(kPanelThreads), 0, st, A, n, kb, info);
         const int m = nt - kb - 1;
         if (m > 0)
             hipLaunchKernelGGL((k_potrf_update<T>), dim3(m * (m + 1) / 2), dim3(256), 0, st, A, n, kb);
@@ -168,6 +182,7 @@ __global__ void k_trmv(const T* __restrict__ L, int n, const T* __restrict__ x, 
     if (i >= n) return;
     const T* row = L + (int64_t)i * n;
     T acc = T(0);
+#pragma unroll 16
     for (int j = 0; j <= i; ++j) acc = num<T>::fma(row[j], x[j], acc);
     y[i] = acc;
 }
@@ -177,6 +192,7 @@ __global__ void k_trmv_t(const T* __restrict__ L, int n, const T* __restrict__ x
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     T acc = T(0);
+#pragma unroll 16
     for (int j = i; j < n; ++j) acc = num<T>::fma(L[(int64_t)j * n + i], x[j], acc);
     y[i] = acc;
 }
@@ -292,67 +308,119 @@ void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStr
 }
 
 // ---- dense cotangents (f64) -----------------------------------------------------------------
-// W = L^-1, one wave per column c: forward substitution of e_c with the column in LDS.
-// Lt64 is L^T in double (row i of Lt64 = column i of L), so the column reads are contiguous.
-template <typename T>
-__global__ void k_transpose64(const T* __restrict__ L, int n, double* __restrict__ Lt) {
-    const int j = blockIdx.x * 16 + threadIdx.x, i = blockIdx.y * 16 + threadIdx.y;
-    if (i < n && j < n) Lt[(int64_t)j * n + i] = j <= i ? (double)L[(int64_t)i * n + j] : 0.0;
+// W = L^-1 in double. One wave solves kInvCols consecutive columns c0.. (so each row of L it reads
+// serves all of them), left-looking over 64-row blocks: lane l of block r0 first forms
+// acc_c = e_c[r] - sum_{c0<=p<r0} L[r][p] x_c[p] along its own row r = r0+l of L (contiguous
+// reads; x in LDS), then the 64 x 64 diagonal block is solved from registers with the pivots
+// broadcast by readlane.
+constexpr int kInvCols = 1;
+
+// lr[lane] of a 64-entry register row, selected by the lane's own index (a select chain, since
+// registers cannot be indexed at run time).
+__device__ inline double bcast_lane_diag(const double (&lr)[64], int lane) {
+    double v = 1.0;
+#pragma unroll
+    for (int jj = 0; jj < 64; ++jj) v = lane == jj ? lr[jj] : v;
+    return v;
 }
 
-__global__ void __launch_bounds__(64) k_trinv(const double* __restrict__ Lt, int n,
+template <typename T>
+__global__ void __launch_bounds__(64) k_trinv(const T* __restrict__ L, int n,
                                               double* __restrict__ W) {
-    extern __shared__ double sx[];
-    const int c = blockIdx.x, lane = threadIdx.x;
-    for (int r = lane; r < n; r += 64) sx[r] = r == c ? 1.0 : 0.0;
-    __syncthreads();
-    for (int i = c; i < n; ++i) {
-        const double* col = Lt + (int64_t)i * n;
-        const double xi = sx[i] / col[i];
-        __syncthreads();
-        if (lane == 0) sx[i] = xi;
-        for (int r = i + 1 + lane; r < n; r += 64) sx[r] = __builtin_fma(-col[r], xi, sx[r]);
+    extern __shared__ double sx[];  // kInvCols x n
+    const int c0 = blockIdx.x * kInvCols, lane = threadIdx.x;
+    for (int r0 = c0; r0 < n; r0 += 64) {
+        const int r = r0 + lane;
+        const bool live = r < n;
+        const T* row = L + (int64_t)(live ? r : 0) * n;
+        double acc[kInvCols];
+#pragma unroll
+        for (int q = 0; q < kInvCols; ++q) acc[q] = (r == c0 + q) ? 1.0 : 0.0;
+        if (live) {
+#pragma unroll 4
+            for (int p = c0; p < r0; ++p) {
+                const double lp = (double)row[p];
+#pragma unroll
+                for (int q = 0; q < kInvCols; ++q) acc[q] = __builtin_fma(-lp, sx[q * n + p], acc[q]);
+            }
+        }
+        double lr[64];
+#pragma unroll
+        for (int jj = 0; jj < 64; ++jj) lr[jj] = (live && r0 + jj < n) ? (double)row[r0 + jj] : 1.0;
+        // one reciprocal per row: lane l holds 1 / L[r0+l][r0+l]
+        const double rinv = 1.0 / bcast_lane_diag(lr, lane);
+#pragma unroll
+        for (int jj = 0; jj < 64; ++jj) {
+            if (r0 + jj < n) {
+                const double rp = bcast(rinv, jj);
+#pragma unroll
+                for (int q = 0; q < kInvCols; ++q) {
+                    const double xj = bcast(acc[q], jj) * rp;
+                    if (lane == jj) acc[q] = xj;
+                    else if (lane > jj) acc[q] = __builtin_fma(-lr[jj], xj, acc[q]);
+                }
+            }
+        }
+        if (live)
+#pragma unroll
+            for (int q = 0; q < kInvCols; ++q) sx[q * n + r] = acc[q];
         __syncthreads();
     }
-    for (int r = lane; r < n; r += 64) W[(int64_t)r * n + c] = sx[r];
+    for (int q = 0; q < kInvCols; ++q) {
+        const int c = c0 + q;
+        if (c >= n) break;
+        for (int r = lane; r < n; r += 64) W[(int64_t)r * n + c] = r < c ? 0.0 : sx[q * n + r];
+    }
 }
 
-// C[i][j] = sum_{a >= max(i, j)} W[a][i] X[a][j] for lower-triangular W, X (n x n, row-major).
+// C[i][j] = sum_{a >= max(i, j)} W[a][i] X[a][j] for lower-triangular W, X (n x n, row-major):
+// 64 x 64 output tiles, 4 x 4 outputs per thread, 16-row slabs of W and X staged in LDS.
 // lower_only: only tiles with i >= j.
+constexpr int kWT = 64, kWK = 16;
 __global__ void __launch_bounds__(256) k_wtx(const double* __restrict__ W,
                                              const double* __restrict__ X, int n,
                                              double* __restrict__ C, int lower_only) {
-    __shared__ double sW[kTile][kTile + 1];
-    __shared__ double sX[kTile][kTile + 1];
+    __shared__ double sW[kWK][kWT + 1];
+    __shared__ double sX[kWK][kWT + 1];
     const int bi = blockIdx.y, bj = blockIdx.x;
     if (lower_only && bj > bi) return;
-    const int i0 = bi * kTile, j0 = bj * kTile;
-    const int tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;
-    double acc[kTile / 8];
+    const int i0 = bi * kWT, j0 = bj * kWT;
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    double acc[4][4];
 #pragma unroll
-    for (int u = 0; u < kTile / 8; ++u) acc[u] = 0.0;
-    const int a_start = (max(i0, j0) / kTile) * kTile;
-    for (int a0 = a_start; a0 < n; a0 += kTile) {
-        for (int e = threadIdx.x; e < kTile * kTile; e += blockDim.x) {
-            const int r = e / kTile, c = e % kTile;
-            const int a = a0 + r;
-            sW[r][c] = (a < n && i0 + c < n) ? W[(int64_t)a * n + i0 + c] : 0.0;
-            sX[r][c] = (a < n && j0 + c < n) ? X[(int64_t)a * n + j0 + c] : 0.0;
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[u][v] = 0.0;
+    const int a_start = (max(i0, j0) / kWK) * kWK;
+    for (int a0 = a_start; a0 < n; a0 += kWK) {
+        for (int e = threadIdx.x; e < kWK * kWT; e += blockDim.x) {
+            const int rr = e / kWT, cc = e % kWT;
+            const int a = a0 + rr;
+            sW[rr][cc] = (a < n && i0 + cc < n) ? W[(int64_t)a * n + i0 + cc] : 0.0;
+            sX[rr][cc] = (a < n && j0 + cc < n) ? X[(int64_t)a * n + j0 + cc] : 0.0;
         }
         __syncthreads();
 #pragma unroll
-        for (int u = 0; u < kTile / 8; ++u) {
-            const int ii = ty + 8 * u;
-#pragma unroll 8
-            for (int r = 0; r < kTile; ++r) acc[u] = __builtin_fma(sW[r][ii], sX[r][tx], acc[u]);
+        for (int rr = 0; rr < kWK; ++rr) {
+            double w[4], x[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) w[u] = sW[rr][ty + 16 * u];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) x[v] = sX[rr][tx + 16 * v];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[u][v] = __builtin_fma(w[u], x[v], acc[u][v]);
         }
         __syncthreads();
     }
 #pragma unroll
-    for (int u = 0; u < kTile / 8; ++u) {
-        const int i = i0 + ty + 8 * u, j = j0 + tx;
-        if (i < n && j < n) C[(int64_t)i * n + j] = acc[u];
-    }
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int i = i0 + ty + 16 * u, j = j0 + tx + 16 * v;
+            if (i < n && j < n) C[(int64_t)i * n + j] = acc[u][v];
+        }
 }
 
 // u = L^T vb (double), h/Q prefix pass: Q[a][j] = u[a] (sum_{j<=b<a} xi[b] W[b][j] + xi[a]W[a][j]/2)
@@ -362,17 +430,34 @@ __global__ void k_ltv64(const T* __restrict__ L, int n, const T* __restrict__ vb
     const int a = blockIdx.x * blockDim.x + threadIdx.x;
     if (a >= n) return;
     double s = 0.0;
+#pragma unroll 16
     for (int i = a; i < n; ++i) s = __builtin_fma((double)L[(int64_t)i * n + a], (double)vb[i], s);
     u[a] = s;
 }
+// Q[a][j] = u[a] (h_j(a) + xi[a] W[a][j] / 2), h_j(a) = sum_{b<a} xi[b] W[b][j] (W is lower
+// triangular, so rows above j add zeros). Workgroup = 32 columns x 8 row chunks: chunk sums,
+// an exclusive prefix over the chunks in LDS, then the running sum within each chunk.
 template <typename T>
-__global__ void k_qprefix(const double* __restrict__ W, int n, const T* __restrict__ xi,
-                          const double* __restrict__ u, double* __restrict__ Q) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= n) return;
-    for (int a = 0; a < j; ++a) Q[(int64_t)a * n + j] = 0.0;
+__global__ void __launch_bounds__(256) k_qprefix(const double* __restrict__ W, int n,
+                                                 const T* __restrict__ xi,
+                                                 const double* __restrict__ u,
+                                                 double* __restrict__ Q) {
+    __shared__ double part[8][33];
+    const int jl = threadIdx.x % 32, ck = threadIdx.x / 32;
+    const int j = blockIdx.x * 32 + jl;
+    const int clen = (n + 7) / 8;
+    const int a_lo = ck * clen, a_hi = min(n, a_lo + clen);
+    double s = 0.0;
+    if (j < n)
+#pragma unroll 8
+        for (int a = a_lo; a < a_hi; ++a) s += W[(int64_t)a * n + j] * (double)xi[a];
+    part[ck][jl] = s;
+    __syncthreads();
     double h = 0.0;
-    for (int a = j; a < n; ++a) {
+    for (int q = 0; q < ck; ++q) h += part[q][jl];
+    if (j >= n) return;
+#pragma unroll 8
+    for (int a = a_lo; a < a_hi; ++a) {
         const double w = W[(int64_t)a * n + j] * (double)xi[a];
         Q[(int64_t)a * n + j] = u[a] * (h + 0.5 * w);
         h += w;
@@ -451,9 +536,9 @@ static void launch_dense_scatter(const Graph& g, const Table<T>& tb, const doubl
 }
 
 template <typename T>
-static void dense_inverse64(const T* L, int n, double* W, double* Lt, hipStream_t st) {
-    hipLaunchKernelGGL((k_transpose64<T>), dim3(cdiv(n, 16), cdiv(n, 16)), dim3(16, 16), 0, st, L, n, Lt);
-    hipLaunchKernelGGL(k_trinv, dim3(n), dim3(64), (size_t)n * sizeof(double), st, Lt, n, W);
+static void dense_inverse64(const T* L, int n, double* W, double* /*scratch*/, hipStream_t st) {
+    hipLaunchKernelGGL((k_trinv<T>), dim3(cdiv(n, kInvCols)), dim3(64),
+                       (size_t)kInvCols * n * sizeof(double), st, L, n, W);
 }
 
 // d(sum log diag L)/dvals: Kinv = W^T W, diagonal halved (src/dense.jl:153-183).
@@ -462,7 +547,7 @@ void dense_grad_logdet(const Graph& g, const Table<T>& tb, const T* L, double* W
                        double* hist_partial, int nw, hipStream_t st) {
     const int n = (int)g.n0;
     dense_inverse64(L, n, W, C, st);  // C doubles as the L^T scratch
-    const dim3 grid(cdiv(n, kTile), cdiv(n, kTile));
+    const dim3 grid(cdiv(n, kWT), cdiv(n, kWT));
     hipLaunchKernelGGL(k_wtx, grid, dim3(256), 0, st, W, W, n, C, 1);
     launch_dense_scatter<T, DM_LOGDET>(g, tb, C, nullptr, hist_partial, nw, st);
 }
@@ -477,8 +562,8 @@ void dense_grad_generate(const Graph& g, const Table<T>& tb, const T* L, const T
     const int n = (int)g.n0;
     dense_inverse64(L, n, W, C, st);
     hipLaunchKernelGGL((k_ltv64<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, L, n, vb, u);
-    hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, W, n, xi, u, Q);
-    const dim3 grid(cdiv(n, kTile), cdiv(n, kTile));
+    hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 32)), dim3(256), 0, st, W, n, xi, u, Q);
+    const dim3 grid(cdiv(n, kWT), cdiv(n, kWT));
     hipLaunchKernelGGL(k_wtx, grid, dim3(256), 0, st, W, Q, n, C, 0);
     launch_dense_scatter<T, DM_GENERATE>(g, tb, C, nullptr, hist_partial, nw, st);
 }

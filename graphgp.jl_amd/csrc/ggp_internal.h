@@ -24,6 +24,7 @@ struct Graph {
     int64_t* rev_ptr = nullptr;    // N+1: consumers of point q are rev[rev_ptr[q] .. rev_ptr[q+1])
     uint32_t* rev = nullptr;       // m*K + j of each consumer, by decreasing consumer position
     std::vector<int64_t> offsets;  // host copy, offsets[0] = n0
+    std::vector<int> rev_group;    // lanes per point of the reverse sweep, per level (0 = dense)
 };
 
 // Device-resident covariance table prepared for O(1) segment lookup.
@@ -52,7 +53,7 @@ struct PointK {
     static void sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
                           const T* sd, int64_t m_lo, int64_t len, hipStream_t st);
     static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                          int64_t q_lo, int64_t q_hi, hipStream_t st);
+                          int64_t q_lo, int64_t q_hi, int G, hipStream_t st);
 };
 extern template struct PointK<float, 4>;
 extern template struct PointK<float, 8>;
@@ -78,7 +79,7 @@ template <typename T>
 void launch_sumsq_half(const T* x, int64_t n, double* out, hipStream_t st);
 template <typename T>
 void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                      int64_t q_lo, int64_t q_hi, hipStream_t st);
+                      int64_t q_lo, int64_t q_hi, int G, hipStream_t st);
 template <typename T>
 void launch_reduce_hist(T* d_out, const double* partial, int nw, int nb, const double* extra,
                         hipStream_t st);

@@ -17,16 +17,23 @@ __device__ inline double block_sum_g(double v, double* s_red) {
     return t;
 }
 
-// d_out[i] = T(sum_w partial[w][i] + extra[i]); one thread per bin, fixed order over w.
+// d_out[i] = T(sum_w partial[w][i] + extra[i]). One wave per bin: lane l sums rows l, l+64, ...
+// in order, then the 64 lane sums are combined by a fixed shuffle tree (deterministic).
 template <typename T>
-__global__ void k_reduce_hist(T* __restrict__ d_out, const double* __restrict__ partial, int nw,
-                              int nb, const double* __restrict__ extra) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nb) return;
+__global__ void __launch_bounds__(256) k_reduce_hist(T* __restrict__ d_out,
+                                                     const double* __restrict__ partial, int nw,
+                                                     int nb, const double* __restrict__ extra) {
+    const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int l = threadIdx.x & 63;
     double s = 0.0;
-    for (int w = 0; w < nw; ++w) s += partial[(size_t)w * nb + i];
-    if (extra) s += extra[i];
-    d_out[i] = (T)s;
+    if (i < nb)
+        for (int w = l; w < nw; w += 64) s += partial[(size_t)w * nb + i];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_down(s, o, 64);
+    if (i < nb && l == 0) {
+        if (extra) s += extra[i];
+        d_out[i] = (T)s;
+    }
 }
 
 // out[0] = sum of n doubles (single block, fixed order per thread then tree).
@@ -121,8 +128,8 @@ void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T
 
 template <typename T>
 void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                      int64_t q_lo, int64_t q_hi, hipStream_t st) {
-#define CALLR(KK) PointK<T, KK>::sweep_rev(g, vb, vbar, xg, mv, sd, q_lo, q_hi, st)
+                      int64_t q_lo, int64_t q_hi, int G, hipStream_t st) {
+#define CALLR(KK) PointK<T, KK>::sweep_rev(g, vb, vbar, xg, mv, sd, q_lo, q_hi, G, st)
     GGP_FOR_K(CALLR);
 #undef CALLR
 }
@@ -130,7 +137,7 @@ void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, 
 template <typename T>
 void launch_reduce_hist(T* d_out, const double* partial, int nw, int nb, const double* extra,
                         hipStream_t st) {
-    hipLaunchKernelGGL((k_reduce_hist<T>), dim3(grid_for(nb)), dim3(kBlock), 0, st, d_out,
+    hipLaunchKernelGGL((k_reduce_hist<T>), dim3((nb + 3) / 4), dim3(256), 0, st, d_out,
                        partial, nw, nb, extra);
 }
 
@@ -164,7 +171,7 @@ void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st) {
     template void launch_sweep_fwd<T>(const Graph&, T*, const T*, int64_t, const T*, const T*, \
                                       int64_t, int64_t, hipStream_t);                          \
     template void launch_sweep_rev<T>(const Graph&, T*, const T*, T*, const T*, const T*,      \
-                                      int64_t, int64_t, hipStream_t);                          \
+                                      int64_t, int64_t, int, hipStream_t);                     \
     template void launch_reduce_hist<T>(T*, const double*, int, int, const double*,            \
                                         hipStream_t);                                          \
     template void launch_gather<T>(T*, const T*, const int32_t*, int64_t, hipStream_t);        \

@@ -127,23 +127,44 @@ k_sweep_fwd(T* __restrict__ v, const T* __restrict__ xi, int64_t xi_off,
 // consumers (p, j) of q of mv_j(p)*vb[p], the consumers listed by decreasing p — exactly the
 // order in which the reference's serial host sweep (src/grad.jl:433-445) adds them — and
 // xg[q] = std_q*vb[q] for refined q. Every consumer lies in a later level, so vb[p] is final.
+//
+// A group of G lanes (G a power of two <= 64, sized to the level's largest fan-in) serves one
+// point: each lane loads one consumer's product mv*vb per round, so the dependent memory round
+// trips per point drop from the fan-in to fan-in/G; the products are then added one by one in
+// list order (shuffled from their lanes), which keeps every rounding of the serial sum.
 template <typename T, int K>
 __global__ void __launch_bounds__(kBlock)
 k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
             const T* __restrict__ mv, const T* __restrict__ sd,
             const int64_t* __restrict__ rev_ptr, const uint32_t* __restrict__ rev,
-            int64_t M, int64_t n0, int64_t q_lo, int64_t q_hi) {
-    const int64_t q = q_lo + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= q_hi) return;
-    T acc = vbar[q];
-    const int64_t e1 = rev_ptr[q + 1];
-    for (int64_t e = rev_ptr[q]; e < e1; ++e) {
-        const uint32_t c = rev[e];
-        const uint32_t m = c / (uint32_t)K, j = c - m * (uint32_t)K;
-        acc = acc + mv[(int64_t)j * M + m] * vb[n0 + m];
+            int64_t M, int64_t n0, int64_t q_lo, int64_t q_hi, int G) {
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int gl = lane & (G - 1);          // lane within the group
+    const int gbase = lane - gl;            // first lane of the group
+    const int64_t q = q_lo + tid / G;
+    const bool live = q < q_hi;
+    int64_t e0 = 0, cnt = 0;
+    T acc = T(0);
+    if (live) {
+        e0 = rev_ptr[q];
+        cnt = rev_ptr[q + 1] - e0;
+        acc = vbar[q];
     }
-    vb[q] = acc;
-    if (xg && q >= n0) xg[q] = sd[q - n0] * acc;
+    for (int64_t base = 0; base < cnt; base += G) {
+        T prod = T(0);
+        if (base + gl < cnt) {
+            const uint32_t c = rev[e0 + base + gl];
+            const uint32_t m = c / (uint32_t)K, j = c - m * (uint32_t)K;
+            prod = mv[(int64_t)j * M + m] * vb[n0 + m];
+        }
+        const int64_t take = cnt - base < G ? cnt - base : G;
+        for (int i = 0; i < take; ++i) acc = acc + __shfl(prod, gbase + i, 64);
+    }
+    if (live && gl == 0) {
+        vb[q] = acc;
+        if (xg && q >= n0) xg[q] = sd[q - n0] * acc;
+    }
 }
 
 // ---- adjoint pullback -----------------------------------------------------------------------
@@ -327,9 +348,9 @@ void PointK<T, K>::sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, 
 
 template <typename T, int K>
 void PointK<T, K>::sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv,
-                             const T* sd, int64_t q_lo, int64_t q_hi, hipStream_t st) {
-    hipLaunchKernelGGL((k_sweep_rev<T, K>), dim3(grid_for_pt(q_hi - q_lo)), dim3(kBlock), 0, st,
-                       vb, vbar, xg, mv, sd, g.rev_ptr, g.rev, g.M, g.n0, q_lo, q_hi);
+                             const T* sd, int64_t q_lo, int64_t q_hi, int G, hipStream_t st) {
+    hipLaunchKernelGGL((k_sweep_rev<T, K>), dim3(grid_for_pt((q_hi - q_lo) * G)), dim3(kBlock), 0,
+                       st, vb, vbar, xg, mv, sd, g.rev_ptr, g.rev, g.M, g.n0, q_lo, q_hi, G);
 }
 
 }  // namespace ggp
