@@ -64,6 +64,19 @@ def factor_algorithmic(k, D, es=4):
     return bytes_, flops
 
 
+def measured_traffic():
+    """HBM bytes per k_factor launch from the committed counter summary (two rocprofv3 --pmc
+    passes, FETCH_SIZE and WRITE_SIZE, calibrated against a copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "k_factor_pmc_1M_k8_f32.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(prob, xi, vb, nthreads):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -91,6 +104,9 @@ def main():
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--ops", default="generate,grad_xi,grad_vals")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="run one 256 MiB device copy first (the known-size reference kernel for "
+                         "calibrating HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); the path's multi-GPU "
@@ -100,6 +116,13 @@ def main():
     import torch
     import graphgp_hip as G
     from graphgp_hip import _native as nat
+
+    if args.calib_copy:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     N, D, n0, k, nbins = args.n, 3, 1000, 8, 1000
     prob, xi_np, vb_np = workload(N, D, n0, k, nbins)
@@ -146,7 +169,7 @@ def main():
     achieved = fb * M / (fac_ms * 1e-3)
     roofline = {"kernel": "k_factor (mean_vec + std for all refined points)", "bound": "hbm",
                 "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK, "traffic": None,
+                "frac": achieved / HBM_PEAK, "traffic": measured_traffic(), "traffic_unit": "bytes per launch",
                 "algorithmic_bytes_per_point": fb, "points_per_launch": M,
                 "flop_frac_fp32": ff * M / (fac_ms * 1e-3) / FP32_PEAK,
                 "avg_launch_ms": fac_ms}

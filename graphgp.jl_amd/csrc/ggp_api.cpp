@@ -180,6 +180,8 @@ int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
     tb.P = P;
     tb.bins.assign(bins, bins + nb);
     tb.vals.assign(vals, vals + nb);
+    tb.aniso = AnisoArgs<T>{};
+    tb.aniso_host.clear();
     if (h->hist_nb != (int)nb) {
         if (dmalloc(h, (void**)&h->hist,
                     (size_t)(h->nblk_pull + h->nw_dense) * (size_t)nb * sizeof(double)))
@@ -218,6 +220,46 @@ void tcollect(ggp_graph* h) {
         }
 }
 
+// Anisotropic table (src/aniso.jl:22-37, src/types.jl:15-20). The grid is used as given
+// (build_anisotropic_covariance's jitter already applied by the caller).
+template <typename T>
+int set_cov_aniso(ggp_graph* h, const T* sb, int64_t ns, const T* zb, int64_t nz, const T* grid,
+                  double alpha) {
+    if (ns < 1 || nz < 1 || ns > 65536 || nz > 65536) return fail(GGP_ERR_ARG, "bad aniso grid size");
+    if (!(std::isfinite(alpha) && alpha > 0)) return fail(GGP_ERR_ARG, "alpha must be finite and > 0");
+    for (int64_t i = 1; i < ns; ++i)
+        if (!(sb[i] > sb[i - 1])) return fail(GGP_ERR_ARG, "spatial_bins must be strictly increasing");
+    for (int64_t i = 1; i < nz; ++i)
+        if (!(zb[i] > zb[i - 1])) return fail(GGP_ERR_ARG, "z_bins must be strictly increasing");
+    if (h->g.D < 2) return fail(GGP_ERR_D, "anisotropic covariance needs D >= 2");
+    if (!(sb[0] >= T(0)) || !(zb[0] >= T(0))) return fail(GGP_ERR_ARG, "aniso axes must start at >= 0");
+    Table<T>& tb = table<T>(h);
+    std::vector<T> host;
+    host.insert(host.end(), sb, sb + ns);
+    host.insert(host.end(), zb, zb + nz);
+    host.insert(host.end(), grid, grid + ns * nz);
+    for (const T& x : host)
+        if (!std::isfinite(x)) return fail(GGP_ERR_ARG, "aniso table must be finite");
+    T* dev = nullptr;
+    if (dmalloc(h, (void**)&dev, host.size() * sizeof(T))) return GGP_ERR_HIP;
+    HC(hipMemcpy(dev, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice));
+    tb.aniso.sb = dev;
+    tb.aniso.zb = dev + ns;
+    tb.aniso.grid = dev + ns + nz;
+    tb.aniso.ns = (int)ns;
+    tb.aniso.nz = (int)nz;
+    tb.aniso.alpha = (T)alpha;
+    tb.aniso_host = host;
+    // the isotropic table is not used by an anisotropic problem
+    tb.vals.assign(1, grid[0]);
+    h->has_cov = true;
+    return 0;
+}
+
+bool is_aniso(ggp_graph* h) {
+    return h->dtype == GGP_F32 ? h->tf.aniso.grid != nullptr : h->td.aniso.grid != nullptr;
+}
+
 // ---- stream plumbing -------------------------------------------------------------------------
 int enter(ggp_graph* h, hipStream_t user) {
     HC(hipSetDevice(h->dev));
@@ -251,6 +293,17 @@ int finish(ggp_graph* h, hipStream_t user) {
 
 template <typename T> T* tp(void* p) { return static_cast<T*>(p); }
 
+// K(0, 0) of the anisotropic table on the host, evaluated as aniso_lookup does (src/aniso.jl:66-84):
+// both fractional indices are 0, so the result is grid[0][0] combined with zero weights.
+template <typename T>
+T dense_aniso_diag(const Table<T>& tb) {
+    const int nz = tb.aniso.nz, ns = tb.aniso.ns;
+    const T* g = tb.aniso_host.data() + ns + nz;
+    const int i1 = ns > 1 ? 1 : 0, j1 = nz > 1 ? 1 : 0;
+    volatile T one = T(1), zero = T(0);
+    return (g[0] * (one - zero) + g[i1 * nz] * zero) * (one - zero) + (g[j1] * (one - zero) + g[i1 * nz + j1] * zero) * zero;
+}
+
 // Dense factor with jitter escalation (src/dense.jl:46-67), synchronous; used after the first
 // in-op attempt reported a non-positive pivot.
 template <typename T>
@@ -258,7 +311,8 @@ int dense_retry(ggp_graph* h) {
     const Table<T>& tb = table<T>(h);
     const int n = (int)h->g.n0;
     T dmean = T(0);
-    for (int i = 0; i < n; ++i) dmean += tb.vals[0];  // every diagonal entry is vals[1]
+    const T d0 = tb.aniso.grid ? dense_aniso_diag(tb) : tb.vals[0];
+    for (int i = 0; i < n; ++i) dmean += d0;  // every diagonal entry is K(0)
     dmean = dmean / T(n > 1 ? n : 1);
     T e = T(1e-9);
     while (e <= T(1e-2)) {
@@ -328,7 +382,7 @@ void sweep_forward(ggp_graph* h, T* v, const T* xi, int64_t xi_off, hipStream_t 
         const int64_t len = g.offsets[b] - g.offsets[b - 1];
         if (len <= 0) continue;
         launch_sweep_fwd<T>(g, v, xi, xi_off, tp<T>(h->mv), tp<T>(h->sd), g.offsets[b - 1] - g.n0,
-                            len, st);
+                            len, table<T>(h).aniso.grid != nullptr, st);
     }
     tstop(h, TM_SWEEP_FWD, st);
 }
@@ -525,6 +579,9 @@ template <typename T>
 int op_grad_vals(ggp_graph* h, int mode, int dkind, const T* in1, const T* in2, T* d_vals,
                  double* scalar_out, hipStream_t user) {
     if (int rc = check_ready(h)) return rc;
+    if (is_aniso(h))
+        return fail(GGP_ERR_ARG, "gradients w.r.t. the covariance table are defined for the "
+                                 "isotropic table only (the anisotropic path is forward-only)");
     if (dkind != DG_NONE)
         if (int rc = ensure_dense64(h)) return rc;
     if (int rc = enter(h, user)) return rc;
@@ -796,6 +853,14 @@ int ggp_kernel_timer_read(const ggp_graph* h, const char* name, double* total_ms
             return 0;
         }
     return fail(GGP_ERR_ARG, std::string("unknown timer ") + name);
+}
+
+int ggp_set_cov_aniso(ggp_graph* h, const void* spatial_bins_host, int64_t n_s,
+                      const void* z_bins_host, int64_t n_z, const void* grid_host, double alpha) {
+    if (!h || !spatial_bins_host || !z_bins_host || !grid_host) return fail(GGP_ERR_ARG, "null argument");
+    if (hipSetDevice(h->dev) != hipSuccess) return fail(GGP_ERR_HIP, "hipSetDevice failed");
+    return DISPATCH(h, set_cov_aniso<float>(h, (const float*)spatial_bins_host, n_s, (const float*)z_bins_host, n_z, (const float*)grid_host, alpha),
+                    set_cov_aniso<double>(h, (const double*)spatial_bins_host, n_s, (const double*)z_bins_host, n_z, (const double*)grid_host, alpha));
 }
 
 int ggp_set_cov_iso(ggp_graph* h, const void* bins_host, const void* vals_host, int64_t nbins) {

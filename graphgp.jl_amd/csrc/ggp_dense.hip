@@ -25,22 +25,26 @@ __device__ inline double bcast(double x, int lane) {
 static inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ---- assembly (src/dense.jl:15-40) ----------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, bool ANISO>
 __global__ void k_dense_assemble(T* __restrict__ A, const uint32_t* __restrict__ coords, int n,
                                  T scale, const TabEnt<T>* __restrict__ tab,
-                                 const uint16_t* __restrict__ acc, const TabParams<T>* __restrict__ Pp, T diag_add) {
-    const TabParams<T> P = *Pp;
+                                 const uint16_t* __restrict__ acc, const TabParams<T>* __restrict__ Pp, T diag_add,
+                                 AnisoArgs<T> an) {
     const int j = blockIdx.x * 16 + threadIdx.x;
     const int i = blockIdx.y * 16 + threadIdx.y;
     if (i >= n || j > i) return;
+    TabParams<T> P{};
+    if (!ANISO) P = *Pp;
     if (i == j) {
-        A[(int64_t)i * n + i] = diag_add == T(0) ? P.v0 : P.v0 + diag_add;
+        const T d0 = ANISO ? aniso_lookup(T(0), T(0), an) : P.v0;
+        A[(int64_t)i * n + i] = diag_add == T(0) ? d0 : d0 + diag_add;
         return;
     }
     uint32_t ci[D], cj[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) { ci[d] = coords[(int64_t)i * D + d]; cj[d] = coords[(int64_t)j * D + d]; }
-    const T v = cov_lookup(radius<T>(sqdist<D>(ci, cj), scale), tab, acc, P);
+    const T v = ANISO ? aniso_pair<T, D>(ci, cj, scale, an)
+                      : cov_lookup(radius<T>(sqdist<D>(ci, cj), scale), tab, acc, P);
     A[(int64_t)i * n + j] = v;
     A[(int64_t)j * n + i] = v;
 }
@@ -299,12 +303,19 @@ void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStr
     const int n = (int)g.n0;
     const dim3 grid(cdiv(n, 16), cdiv(n, 16)), blk(16, 16);
     const T scale = (T)g.scale;
+    const bool an = tb.aniso.grid != nullptr;
+#define GGP_ASM(DD)                                                                             \
+    do {                                                                                        \
+        if (an) hipLaunchKernelGGL((k_dense_assemble<T, DD, true>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso); \
+        else hipLaunchKernelGGL((k_dense_assemble<T, DD, false>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso); \
+    } while (0)
     switch (g.D) {
-        case 2: hipLaunchKernelGGL((k_dense_assemble<T, 2>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add); break;
-        case 3: hipLaunchKernelGGL((k_dense_assemble<T, 3>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add); break;
-        case 4: hipLaunchKernelGGL((k_dense_assemble<T, 4>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add); break;
+        case 2: GGP_ASM(2); break;
+        case 3: GGP_ASM(3); break;
+        case 4: GGP_ASM(4); break;
         default: break;
     }
+#undef GGP_ASM
 }
 
 // ---- dense cotangents (f64) -----------------------------------------------------------------

@@ -35,6 +35,8 @@ struct Table {
     uint16_t* acc = nullptr;    // ucells+1 entries
     TabParams<T> P{};
     std::vector<T> bins, vals;  // host copies
+    AnisoArgs<T> aniso{};        // device arrays of the anisotropic table (grid == null: isotropic)
+    std::vector<T> aniso_host;   // host copy: [sb, zb, grid]
 };
 
 enum FactorMode { F_MV = 1, F_TERMS = 2, F_INV = 4 };
@@ -51,7 +53,7 @@ struct PointK {
                          const T* vb, double* hist_partial, double* scalar_partial,
                          unsigned nblk, hipStream_t st);
     static void sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                          const T* sd, int64_t m_lo, int64_t len, hipStream_t st);
+                          const T* sd, int64_t m_lo, int64_t len, bool two_pass, hipStream_t st);
     static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
                           int64_t q_lo, int64_t q_hi, int G, hipStream_t st);
 };
@@ -74,7 +76,7 @@ void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, c
                      hipStream_t st);
 template <typename T>
 void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                      const T* sd, int64_t m_lo, int64_t len, hipStream_t st);
+                      const T* sd, int64_t m_lo, int64_t len, bool two_pass, hipStream_t st);
 template <typename T>
 void launch_sumsq_half(const T* x, int64_t n, double* out, hipStream_t st);
 template <typename T>

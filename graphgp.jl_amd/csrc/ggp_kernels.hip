@@ -120,8 +120,8 @@ void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, c
 
 template <typename T>
 void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                      const T* sd, int64_t m_lo, int64_t len, hipStream_t st) {
-#define CALLS(KK) PointK<T, KK>::sweep_fwd(g, v, xi, xi_off, mv, sd, m_lo, len, st)
+                      const T* sd, int64_t m_lo, int64_t len, bool two_pass, hipStream_t st) {
+#define CALLS(KK) PointK<T, KK>::sweep_fwd(g, v, xi, xi_off, mv, sd, m_lo, len, two_pass, st)
     GGP_FOR_K(CALLS);
 #undef CALLS
 }
@@ -169,7 +169,7 @@ void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st) {
     template void launch_pullback<T>(const Graph&, const Table<T>&, int, const T*, const T*,   \
                                      const T*, double*, double*, unsigned, hipStream_t);       \
     template void launch_sweep_fwd<T>(const Graph&, T*, const T*, int64_t, const T*, const T*, \
-                                      int64_t, int64_t, hipStream_t);                          \
+                                      int64_t, int64_t, bool, hipStream_t);                    \
     template void launch_sweep_rev<T>(const Graph&, T*, const T*, T*, const T*, const T*,      \
                                       int64_t, int64_t, int, hipStream_t);                     \
     template void launch_reduce_hist<T>(T*, const double*, int, int, const double*,            \

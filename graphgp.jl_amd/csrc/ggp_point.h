@@ -119,6 +119,60 @@ __device__ inline T radius(double sq, T scale) {
     return num<T>::sqrt((T)sq) * scale;
 }
 
+// ---- anisotropic covariance K(d_spatial, d_z) (src/aniso.jl) ----------------------------------
+// Device view of the table: axes sb (ns), zb (nz), grid[i*nz + j] = K(sb[i], zb[j]), alpha.
+template <typename T> struct AnisoArgs {
+    const T* sb = nullptr;
+    const T* zb = nullptr;
+    const T* grid = nullptr;
+    int ns = 0, nz = 0;
+    T alpha = T(1);
+};
+
+// _frac_index (src/aniso.jl:43-57): 0-based fractional position of d on an increasing axis,
+// clamped to [0, n-1]; the bracketing segment is the binary search's (Julia tie rule).
+template <typename T>
+__device__ inline T frac_index(T d, const T* __restrict__ bins, int n) {
+    if (d <= bins[0]) return T(0);
+    if (d >= bins[n - 1]) return T(n - 1);
+    int lo = 0, hi = n - 1;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (bins[mid] <= d) lo = mid; else hi = mid;
+    }
+    const T x0 = bins[lo], x1 = bins[lo + 1];
+    return T(lo) + (d - x0) / (x1 - x0);
+}
+
+// aniso_lookup (src/aniso.jl:66-84): bilinear interpolation with edge clamping; no @fastmath.
+template <typename T>
+__device__ inline T aniso_lookup(T ds, T dz, const AnisoArgs<T>& a) {
+    const T fx = frac_index(ds, a.sb, a.ns), fz = frac_index(dz, a.zb, a.nz);
+    const int i0 = (int)fx, j0 = (int)fz;
+    const int i1 = i0 + 1 < a.ns ? i0 + 1 : a.ns - 1, j1 = j0 + 1 < a.nz ? j0 + 1 : a.nz - 1;
+    const T tx = fx - T(i0), tz = fz - T(j0);
+    const T g00 = a.grid[i0 * a.nz + j0], g10 = a.grid[i1 * a.nz + j0];
+    const T g01 = a.grid[i0 * a.nz + j1], g11 = a.grid[i1 * a.nz + j1];
+    return (g00 * (T(1) - tx) + g10 * tx) * (T(1) - tz) + (g01 * (T(1) - tx) + g11 * tx) * tz;
+}
+
+// Pair covariance of two lattice points (src/aniso.jl:96-106): spatial distance over the first
+// D-1 dims, radial |dz| * scale / alpha over the last.
+template <typename T, int D>
+__device__ inline T aniso_pair(const uint32_t (&a)[D], const uint32_t (&b)[D], T scale,
+                               const AnisoArgs<T>& an) {
+    double sqs = 0.0;
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d) {
+        const double x = (double)((int32_t)a[d] - (int32_t)b[d]);
+        sqs = __builtin_fma(x, x, sqs);  // exact integers
+    }
+    const T dz = (T)((int32_t)a[D - 1] - (int32_t)b[D - 1]);  // exact: |dz| < 2^24
+    const T d_spatial = num<T>::sqrt((T)sqs) * scale;
+    const T d_z = __builtin_fabs(dz) * scale / an.alpha;
+    return aniso_lookup(d_spatial, d_z, an);
+}
+
 // ---- the per-point block ------------------------------------------------------------------
 template <typename T, int K, int D>
 struct Block {
@@ -154,6 +208,17 @@ struct Block {
 #pragma unroll
             for (int b = 0; b < a; ++b)
                 A[tri(a, b)] = cov_lookup(radius<T>(sqdist<D>(jc[a], jc[b]), scale), tab, acc, P);
+        }
+    }
+
+    // anisotropic assemble_cov! (src/aniso.jl:88-108).
+    __device__ inline void assemble_aniso(T scale, const AnisoArgs<T>& an) {
+        const T diagv = aniso_lookup(T(0), T(0), an);
+#pragma unroll
+        for (int a = 0; a < N; ++a) {
+            A[tri(a, a)] = diagv;
+#pragma unroll
+            for (int b = 0; b < a; ++b) A[tri(a, b)] = aniso_pair<T, D>(jc[a], jc[b], scale, an);
         }
     }
 

@@ -49,19 +49,25 @@ __device__ inline double block_sum(double v, double* s_red) {
 }
 
 // ---- factor pass ----------------------------------------------------------------------------
-template <typename T, int K, int D, int MODE>
+// ANISO: the covariance comes from the anisotropic grid (src/aniso.jl) instead of (bins, vals).
+template <typename T, int K, int D, int MODE, bool ANISO>
 __global__ void __launch_bounds__(kBlock)
 k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, int64_t M,
          int64_t n0, T scale, const TabEnt<T>* __restrict__ g_tab,
          const uint16_t* __restrict__ g_acc, const TabParams<T>* __restrict__ Pp, T* __restrict__ mv,
          T* __restrict__ sd, T* __restrict__ terms, double* __restrict__ partial,
-         const T* __restrict__ values, T* __restrict__ xi_out) {
-    const TabParams<T> P = *Pp;
+         const T* __restrict__ values, T* __restrict__ xi_out, AnisoArgs<T> an) {
     extern __shared__ __align__(16) unsigned char smem[];
-    TabEnt<T>* s_tab = reinterpret_cast<TabEnt<T>*>(smem);
-    uint16_t* s_acc = reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
     __shared__ double s_red[kBlock / 64];
-    stage_table(s_tab, s_acc, g_tab, g_acc, P);
+    TabParams<T> P{};
+    TabEnt<T>* s_tab = nullptr;
+    uint16_t* s_acc = nullptr;
+    if (!ANISO) {
+        P = *Pp;
+        s_tab = reinterpret_cast<TabEnt<T>*>(smem);
+        s_acc = reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
+        stage_table(s_tab, s_acc, g_tab, g_acc, P);
+    }
 
     double lsum = 0.0;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -69,7 +75,8 @@ k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, i
         Block<T, K, D> blk;
         int32_t nb[K];
         blk.gather(coords, nbr, M, m, n0, nb);
-        blk.assemble(scale, s_tab, s_acc, P);
+        if (ANISO) blk.assemble_aniso(scale, an);
+        else blk.assemble(scale, s_tab, s_acc, P);
         blk.cholesky();
         const T s = blk.stddev();
         if (MODE & F_TERMS) {
@@ -102,7 +109,9 @@ k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, i
 // ---- level sweeps ---------------------------------------------------------------------------
 // Forward apply of one depth level (src/kernels.jl:113-118): std*xi first, then + mv_j*v_j in
 // neighbour order, each product rounded before the add (that code is not under @fastmath).
-template <typename T, int K>
+// TWO_PASS: the anisotropic apply order (src/kernels.jl:89-92): sum mv_j*v_j first, then
+// + std*xi.
+template <typename T, int K, bool TWO_PASS>
 __global__ void __launch_bounds__(kBlock)
 k_sweep_fwd(T* __restrict__ v, const T* __restrict__ xi, int64_t xi_off,
             const T* __restrict__ mv, const T* __restrict__ sd, const int32_t* __restrict__ nbr,
@@ -117,10 +126,17 @@ k_sweep_fwd(T* __restrict__ v, const T* __restrict__ xi, int64_t xi_off,
         nb[j] = nbr[(int64_t)j * M + m];
         w[j] = mv[(int64_t)j * M + m];
     }
-    T acc = sd[m] * xi[xi_off + m];
+    if (TWO_PASS) {
+        T acc = T(0);
 #pragma unroll
-    for (int j = 0; j < K; ++j) acc = acc + w[j] * v[nb[j]];
-    v[n0 + m] = acc;
+        for (int j = 0; j < K; ++j) acc = acc + w[j] * v[nb[j]];
+        v[n0 + m] = acc + sd[m] * xi[xi_off + m];
+    } else {
+        T acc = sd[m] * xi[xi_off + m];
+#pragma unroll
+        for (int j = 0; j < K; ++j) acc = acc + w[j] * v[nb[j]];
+        v[n0 + m] = acc;
+    }
 }
 
 // Reverse sweep of one depth level, positions [q_lo, q_hi): vb[q] = vbar[q] + sum over the
@@ -289,12 +305,20 @@ template <typename T, int K>
 void PointK<T, K>::factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
                           double* partial, const T* values, T* xi_out, unsigned nblk,
                           hipStream_t st) {
-    const size_t lds = tab_bytes<T>(tb.P.nb, tb.P.ucells);
+    const bool aniso = tb.aniso.grid != nullptr;
+    const size_t lds = aniso ? 0 : tab_bytes<T>(tb.P.nb, tb.P.ucells);
     const T scale = (T)g.scale;
 #define GGP_FACTOR(DD, MODEV)                                                                  \
-    hipLaunchKernelGGL((k_factor<T, K, DD, MODEV>), dim3(nblk), dim3(kBlock), lds, st,          \
-                       g.coords, g.nbr, g.M, g.n0, scale, tb.tab, tb.acc, tb.params, mv, sd,    \
-                       terms, partial, values, xi_out)
+    do {                                                                                       \
+        if (aniso)                                                                             \
+            hipLaunchKernelGGL((k_factor<T, K, DD, MODEV, true>), dim3(nblk), dim3(kBlock), 0,  \
+                               st, g.coords, g.nbr, g.M, g.n0, scale, tb.tab, tb.acc,           \
+                               tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso);    \
+        else                                                                                   \
+            hipLaunchKernelGGL((k_factor<T, K, DD, MODEV, false>), dim3(nblk), dim3(kBlock),    \
+                               lds, st, g.coords, g.nbr, g.M, g.n0, scale, tb.tab, tb.acc,      \
+                               tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso);    \
+    } while (0)
 #define GGP_FACTOR_D(DD)                                                                       \
     switch (mode) {                                                                            \
         case F_MV: GGP_FACTOR(DD, F_MV); break;                                                \
@@ -341,9 +365,14 @@ void PointK<T, K>::pullback(const Graph& g, const Table<T>& tb, int mode, const 
 
 template <typename T, int K>
 void PointK<T, K>::sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                             const T* sd, int64_t m_lo, int64_t len, hipStream_t st) {
-    hipLaunchKernelGGL((k_sweep_fwd<T, K>), dim3(grid_for_pt(len)), dim3(kBlock), 0, st, v, xi,
-                       xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len);
+                             const T* sd, int64_t m_lo, int64_t len, bool two_pass,
+                             hipStream_t st) {
+    if (two_pass)
+        hipLaunchKernelGGL((k_sweep_fwd<T, K, true>), dim3(grid_for_pt(len)), dim3(kBlock), 0, st,
+                           v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len);
+    else
+        hipLaunchKernelGGL((k_sweep_fwd<T, K, false>), dim3(grid_for_pt(len)), dim3(kBlock), 0,
+                           st, v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len);
 }
 
 template <typename T, int K>

@@ -9,7 +9,9 @@ from ._native import GraphGPError, build
 from .extras import hyperparam_grad, make_cov_bins, matern_kernel, rbf_kernel
 from .graph import build_graph, build_graph_arrays
 from .problem import (
+    AnisoCov,
     GraphGPProblem,
+    build_anisotropic_covariance,
     HipProblem,
     check_graph,
     generate,

@@ -48,6 +48,7 @@ _HIP_SIGS = {
     "ggp_graph_shape": (C.c_int, [_P, C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64),
                                   C.POINTER(_I32), C.POINTER(_I64), C.POINTER(_I32)]),
     "ggp_set_cov_iso": (C.c_int, [_P, _P, _P, _I64]),
+    "ggp_set_cov_aniso": (C.c_int, [_P, _P, _I64, _P, _I64, _P, C.c_double]),
     "ggp_kernel_timers": (C.c_int, [_P, _I32]),
     "ggp_kernel_timer_read": (C.c_int, [_P, C.c_char_p, _DP, C.POINTER(_I64)]),
     "ggp_generate": (C.c_int, [_P, _P, _P, _P]),

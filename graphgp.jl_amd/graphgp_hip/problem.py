@@ -30,10 +30,37 @@ import numpy as np
 from . import _native as nat
 
 
-class GraphGPProblem:
-    """Host container: graph + discretized covariance (src/types.jl:22-58)."""
+class AnisoCov:
+    """Anisotropic covariance K(d_spatial, d_z) on a bilinear table (src/types.jl:15-20):
+    spatial_bins (ns,), z_bins (nz,), grid (ns, nz), alpha."""
 
-    def __init__(self, coords, neighbors, offsets, n0, scale, bins, vals, indices=None):
+    def __init__(self, spatial_bins, z_bins, grid, alpha):
+        self.spatial_bins = np.asarray(spatial_bins)
+        self.z_bins = np.asarray(z_bins)
+        self.grid = np.asarray(grid)
+        self.alpha = float(alpha)
+        if self.grid.shape != (len(self.spatial_bins), len(self.z_bins)):
+            raise ValueError("grid must be (length(spatial_bins), length(z_bins))")
+
+
+def build_anisotropic_covariance(spatial_bins, z_bins, grid, alpha, jitter=0.0, dtype=None):
+    """AnisoCov with grid[0, 0] inflated by (1 + jitter) (src/aniso.jl:22-37)."""
+    dt = np.dtype(dtype or np.asarray(grid).dtype)
+    g = np.array(grid, dtype=dt)
+    g[0, 0] = g[0, 0] * (dt.type(1) + dt.type(jitter))
+    return AnisoCov(np.asarray(spatial_bins, dtype=dt), np.asarray(z_bins, dtype=dt), g,
+                    float(alpha))
+
+
+class GraphGPProblem:
+    """Host container: graph + discretized covariance (src/types.jl:22-58). With `cov` set (an
+    AnisoCov) the anisotropic covariance replaces (bins, vals), as in the reference."""
+
+    def __init__(self, coords, neighbors, offsets, n0, scale, bins=None, vals=None, indices=None,
+                 cov=None):
+        if cov is not None and vals is None:
+            bins, vals = cov.spatial_bins, cov.z_bins   # placeholders, as src/types.jl:75-80
+        self.cov = cov
         self.coords = np.ascontiguousarray(coords, dtype=np.uint32)
         self.neighbors = np.ascontiguousarray(neighbors, dtype=np.int64)
         self.offsets = np.ascontiguousarray(offsets, dtype=np.int64)
@@ -127,7 +154,21 @@ class HipProblem:
                  len(prob.offsets), None if idx is None else idx.ctypes.data, prob.n0, prob.K,
                  prob.N, prob.D, prob.scale,
                  nat.GGP_F32 if self.dtype == np.float32 else nat.GGP_F64)
-        self.set_vals(prob.vals, prob.bins)
+        if prob.cov is not None:
+            self.set_aniso(prob.cov)
+        else:
+            self.set_vals(prob.vals, prob.bins)
+
+    def set_aniso(self, cov):
+        """Use the anisotropic covariance (forward-only, as in the reference)."""
+        sb = np.ascontiguousarray(cov.spatial_bins, dtype=self.dtype)
+        zb = np.ascontiguousarray(cov.z_bins, dtype=self.dtype)
+        g = np.ascontiguousarray(cov.grid, dtype=self.dtype)
+        self._aniso_arrays = (sb, zb, g)
+        self.bins = self.vals = None
+        nat.call("ggp_set_cov_aniso", self._h, sb.ctypes.data, len(sb), zb.ctypes.data, len(zb),
+                 g.ctypes.data, float(cov.alpha))
+        return self
 
     def set_vals(self, vals, bins=None):
         """Replace the covariance table (the analogue of _set_vals, src/chainrules.jl:18-21)."""
@@ -168,6 +209,12 @@ def _to_host(x, dtype):
     if hasattr(x, "detach"):
         x = x.detach().cpu().numpy()
     return np.ascontiguousarray(x, dtype=dtype)
+
+
+def _nb(prob):
+    """Length of the d/dvals output. An anisotropic problem has no table to differentiate; the
+    library rejects its d/dvals calls, so a one-element buffer stands in for the output."""
+    return 1 if prob.bins is None else len(prob.bins)
 
 
 def _require(prob):
@@ -292,26 +339,26 @@ def generate_grad_vals(prob, xi, vbar):
     _require(prob)
     x, np_in = _dev(xi, prob.N, prob.dtype)
     vb, _ = _dev(vbar, prob.N, prob.dtype)
-    out = _empty(len(prob.bins), prob.dtype)
+    out = _empty(_nb(prob), prob.dtype)
     nat.call("ggp_generate_grad_vals", prob.handle, _ptr(x), _ptr(vb), _ptr(out), _stream())
-    return _out(out, len(prob.bins), np_in)
+    return _out(out, _nb(prob), np_in)
 
 
 def refine_logdet_grad_vals(prob, as_numpy=True):
     """d(refine_logdet)/dvals (src/grad.jl:96-119)."""
     _require(prob)
-    out = _empty(len(prob.bins), prob.dtype)
+    out = _empty(_nb(prob), prob.dtype)
     nat.call("ggp_refine_logdet_grad_vals", prob.handle, _ptr(out), None, _stream())
-    return _out(out, len(prob.bins), as_numpy)
+    return _out(out, _nb(prob), as_numpy)
 
 
 def generate_logdet_and_grad_vals(prob, as_numpy=True):
     """(generate_logdet, its d/dvals) in one pass (src/grad.jl:680-715)."""
     _require(prob)
-    out = _empty(len(prob.bins), prob.dtype)
+    out = _empty(_nb(prob), prob.dtype)
     ld = C.c_double()
     nat.call("ggp_generate_logdet_grad_vals", prob.handle, _ptr(out), C.byref(ld), _stream())
-    return ld.value, _out(out, len(prob.bins), as_numpy)
+    return ld.value, _out(out, _nb(prob), as_numpy)
 
 
 def generate_logdet_grad_vals(prob, as_numpy=True):
@@ -323,19 +370,19 @@ def refine_inv_loss_grad_vals(prob, values_tree):
     """(0.5*||refine_inv(values)||^2, its d/dvals) (src/grad.jl:626-671)."""
     _require(prob)
     v, np_in = _dev(values_tree, prob.N, prob.dtype)
-    out = _empty(len(prob.bins), prob.dtype)
+    out = _empty(_nb(prob), prob.dtype)
     loss = C.c_double()
     nat.call("ggp_refine_inv_loss_grad_vals", prob.handle, _ptr(v), _ptr(out), C.byref(loss),
              _stream())
-    return loss.value, _out(out, len(prob.bins), np_in)
+    return loss.value, _out(out, _nb(prob), np_in)
 
 
 def generate_inv_loss_grad_vals(prob, data):
     """(0.5*||generate_inv(data)||^2, its d/dvals), data in original order (src/grad.jl:514-529)."""
     _require(prob)
     d, np_in = _dev(data, prob.N, prob.dtype)
-    out = _empty(len(prob.bins), prob.dtype)
+    out = _empty(_nb(prob), prob.dtype)
     loss = C.c_double()
     nat.call("ggp_generate_inv_loss_grad_vals", prob.handle, _ptr(d), _ptr(out), C.byref(loss),
              _stream())
-    return loss.value, _out(out, len(prob.bins), np_in)
+    return loss.value, _out(out, _nb(prob), np_in)

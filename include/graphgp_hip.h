@@ -77,6 +77,16 @@ int ggp_graph_shape(const ggp_graph* h, int64_t* N, int64_t* n0, int64_t* k, int
  * Replacing the table is the analogue of _set_vals (src/chainrules.jl:18-21). */
 int ggp_set_cov_iso(ggp_graph* h, const void* bins_host, const void* vals_host, int64_t nbins);
 
+/* Anisotropic covariance K(d_spatial, d_z) (AnisoCov, src/types.jl:15-20; src/aniso.jl): a
+ * bilinear table grid (n_s x n_z, row-major: grid[i*n_z + j] = K(spatial_bins[i], z_bins[j]))
+ * over the spatial distance of the first D-1 coordinates and |dz| * scale / alpha of the last.
+ * Host arrays of the problem's element type, axes strictly increasing. Replaces any isotropic
+ * table. As in the reference, anisotropic problems are forward-only: generate, generate_inv,
+ * generate_logdet, refine_* and generate_grad_xi (the transpose of the forward map) run; the
+ * d/dvals ops return GGP_ERR_ARG. */
+int ggp_set_cov_aniso(ggp_graph* h, const void* spatial_bins_host, int64_t n_s,
+                      const void* z_bins_host, int64_t n_z, const void* grid_host, double alpha);
+
 /* ---- forward ops -------------------------------------------------------------------------- */
 
 /* generate (src/orchestrate.jl:19-42): out = G(xi), both length N, original order. */

@@ -49,6 +49,13 @@ struct Prob {
     const void* bins;
     const void* vals;
     int nthreads;
+    // anisotropic covariance (src/types.jl:15-20); aniso != 0 selects it over (bins, vals)
+    int aniso;
+    const void* sbins;  // spatial axis, ns entries
+    const void* zbins;  // z axis, nz entries
+    const void* grid;   // ns x nz, row-major: grid[i*nz + j] = K(sbins[i], zbins[j])
+    int64_t ns, nz;
+    double alpha;
 };
 
 template <typename T> inline T eps_of();
@@ -133,6 +140,53 @@ inline void assemble_cov(T* A, const uint32_t* jc, int64_t n, int64_t D, T scale
     }
 }
 
+// ---- src/aniso.jl:43-84 (no @fastmath in these functions) -------------------------------------
+template <typename T>
+inline T frac_index(T d, const T* bins, int64_t n) {
+    if (d <= bins[0]) return T(0);
+    if (d >= bins[n - 1]) return T(n - 1);
+    const int64_t lo = search_lo(d, bins, n);
+    const T x0 = bins[lo], x1 = bins[lo + 1];
+    return T(lo) + (d - x0) / (x1 - x0);
+}
+
+template <typename T>
+inline T aniso_lookup(T ds, T dz, const Prob& p) {
+    const T* sb = (const T*)p.sbins; const T* zb = (const T*)p.zbins; const T* g = (const T*)p.grid;
+    const int64_t ns = p.ns, nz = p.nz;
+    const T fx = frac_index(ds, sb, ns), fz = frac_index(dz, zb, nz);
+    const int64_t i0 = (int64_t)fx, j0 = (int64_t)fz;
+    const int64_t i1 = i0 + 1 < ns ? i0 + 1 : ns - 1, j1 = j0 + 1 < nz ? j0 + 1 : nz - 1;
+    const T tx = fx - T(i0), tz = fz - T(j0);
+    const T g00 = g[i0 * nz + j0], g10 = g[i1 * nz + j0], g01 = g[i0 * nz + j1], g11 = g[i1 * nz + j1];
+    return (g00 * (T(1) - tx) + g10 * tx) * (T(1) - tz) + (g01 * (T(1) - tx) + g11 * tx) * tz;
+}
+
+// Anisotropic pair covariance (src/aniso.jl:88-108): spatial distance over dims 0..D-2, radial
+// |dz| * scale / alpha over the last dim.
+template <typename T>
+inline T aniso_pair(const uint32_t* a, const uint32_t* b, int64_t D, T scale, const Prob& p) {
+    int64_t sqs = 0;
+    for (int64_t d = 0; d < D - 1; ++d) {
+        int64_t di = (int64_t)a[d] - (int64_t)b[d];
+        sqs += di * di;
+    }
+    const int64_t dzi = (int64_t)a[D - 1] - (int64_t)b[D - 1];
+    const T d_spatial = std::sqrt(T(sqs)) * scale;
+    const T d_z = std::abs(T(dzi)) * scale / T(p.alpha);
+    return aniso_lookup(d_spatial, d_z, p);
+}
+
+template <typename T>
+inline void assemble_cov_aniso(T* A, const uint32_t* jc, int64_t n, int64_t D, T scale,
+                               const Prob& p) {
+    const T diagv = aniso_lookup(T(0), T(0), p);
+    for (int64_t a = 0; a < n; ++a) {
+        A[a * n + a] = diagv;
+        for (int64_t b = 0; b < a; ++b) A[a * n + b] = aniso_pair(jc + a * D, jc + b * D, D, scale, p);
+    }
+}
+
 // ---- src/linalg.jl:38-73 --------------------------------------------------------------------
 template <typename T>
 inline void chol_lower(T* A, int64_t n) {
@@ -212,7 +266,8 @@ template <typename T>
 inline void factor_point(Scratch<T>& s, const Prob& p, int64_t m, T scale, const T* bins,
                          const T* vals) {
     gather_joint(s.jc.data(), p, m);
-    assemble_cov(s.A.data(), s.jc.data(), s.n, p.D, scale, bins, vals, p.nbins);
+    if (p.aniso) assemble_cov_aniso(s.A.data(), s.jc.data(), s.n, p.D, scale, p);
+    else assemble_cov(s.A.data(), s.jc.data(), s.n, p.D, scale, bins, vals, p.nbins);
     chol_lower(s.A.data(), s.n);
 }
 
@@ -298,9 +353,32 @@ void refine_meanvec_std(const Prob& p, T* mean_vec, T* sd) {
 
 // ---- src/api.jl:113-141 + src/cpu_native.jl:86-112 (fused per-batch apply) ------------------
 template <typename T>
+void refine_meanvec_std(const Prob& p, T* mean_vec, T* sd);
+
+template <typename T>
 void refine(const Prob& p, T* values, const T* xi_ref) {
     const T* bins = (const T*)p.bins; const T* vals = (const T*)p.vals; const T scale = T(p.scale);
     const int64_t K = p.K, n0 = p.n0;
+    if (p.aniso) {
+        // src/api.jl:143-168: materialise mean_vec/std, then per batch acc = sum mv*v; v = acc + std*xi
+        const int64_t M = p.N - n0;
+        std::vector<T> mv(M * K > 0 ? M * K : 1), sd(M > 0 ? M : 1);
+        refine_meanvec_std(p, mv.data(), sd.data());
+        for (int64_t b = 1; b < p.n_offsets; ++b) {
+            const int64_t m_lo = p.offsets[b - 1] - n0;
+            const int64_t len = p.offsets[b] - p.offsets[b - 1];
+            if (len <= 0) continue;
+            threaded_points(len, p.nthreads, [&](int64_t lo, int64_t hi) {
+                for (int64_t t = lo; t < hi; ++t) {
+                    const int64_t m = m_lo + t;
+                    T acc = T(0);
+                    for (int64_t j = 0; j < K; ++j) acc += mv[m * K + j] * values[p.neighbors[m * K + j]];
+                    values[n0 + m] = acc + sd[m] * xi_ref[m];
+                }
+            });
+        }
+        return;
+    }
     for (int64_t b = 1; b < p.n_offsets; ++b) {
         const int64_t m_lo = p.offsets[b - 1] - n0;
         const int64_t len = p.offsets[b] - p.offsets[b - 1];
@@ -325,6 +403,18 @@ template <typename T>
 void assemble_dense_cov(const Prob& p, int64_t n, T* Kd) {
     const T* bins = (const T*)p.bins; const T* vals = (const T*)p.vals; const T scale = T(p.scale);
     const int64_t D = p.D;
+    if (p.aniso) {  // src/aniso.jl:222-247
+        const T diagv = aniso_lookup(T(0), T(0), p);
+        for (int64_t j = 0; j < n; ++j) {
+            Kd[j * n + j] = diagv;
+            for (int64_t i = j + 1; i < n; ++i) {
+                const T v = aniso_pair(p.coords + i * D, p.coords + j * D, D, scale, p);
+                Kd[i * n + j] = v;
+                Kd[j * n + i] = v;
+            }
+        }
+        return;
+    }
     for (int64_t j = 0; j < n; ++j) {
         Kd[j * n + j] = cov_lookup(T(0), bins, vals, p.nbins);
         for (int64_t i = j + 1; i < n; ++i) {

@@ -36,6 +36,13 @@ class _Prob(C.Structure):
         ("bins", C.c_void_p),
         ("vals", C.c_void_p),
         ("nthreads", C.c_int),
+        ("aniso", C.c_int),
+        ("sbins", C.c_void_p),
+        ("zbins", C.c_void_p),
+        ("grid", C.c_void_p),
+        ("ns", C.c_int64),
+        ("nz", C.c_int64),
+        ("alpha", C.c_double),
     ]
 
 
@@ -66,7 +73,9 @@ class Problem:
     """A refinement problem held in numpy arrays, in the oracle's (and the HIP ABI's) layout."""
 
     def __init__(self, coords, neighbors, offsets, n0, scale, bins, vals, indices=None,
-                 dtype=np.float64, nthreads=None):
+                 dtype=np.float64, nthreads=None, aniso=None):
+        """aniso: optional (spatial_bins, z_bins, grid (ns, nz), alpha) — the anisotropic
+        covariance, which then replaces (bins, vals) (src/aniso.jl)."""
         self.dtype = np.dtype(dtype)
         self.coords = np.ascontiguousarray(coords, dtype=np.uint32)
         self.neighbors = np.ascontiguousarray(neighbors, dtype=np.int64)
@@ -81,20 +90,31 @@ class Problem:
         self.K = self.neighbors.shape[1] if self.neighbors.ndim == 2 else 0
         assert self.neighbors.shape[0] == self.M
         self.nthreads = int(nthreads or os.cpu_count() or 1)
+        self.aniso = aniso
+        if aniso is not None:
+            sb, zb, grid, alpha = aniso
+            self._sb = np.ascontiguousarray(sb, dtype=self.dtype)
+            self._zb = np.ascontiguousarray(zb, dtype=self.dtype)
+            self._grid = np.ascontiguousarray(grid, dtype=self.dtype)
+            assert self._grid.shape == (len(self._sb), len(self._zb))
+            an = (1, _ptr(self._sb), _ptr(self._zb), _ptr(self._grid), len(self._sb),
+                  len(self._zb), float(alpha))
+        else:
+            an = (0, None, None, None, 0, 0, 0.0)
         self._s = _Prob(_ptr(self.coords), _ptr(self.neighbors), _ptr(self.offsets),
                         _ptr(self.indices), len(self.offsets), self.n0, self.K, self.N, self.D,
                         len(self.bins), self.scale, _ptr(self.bins), _ptr(self.vals),
-                        self.nthreads)
+                        self.nthreads, *an)
 
     # the struct keeps raw pointers: keep arrays alive via self
     def with_vals(self, vals):
         return Problem(self.coords, self.neighbors, self.offsets, self.n0, self.scale, self.bins,
-                       vals, self.indices, self.dtype, self.nthreads)
+                       vals, self.indices, self.dtype, self.nthreads, self.aniso)
 
     def with_dtype(self, dtype):
         return Problem(self.coords, self.neighbors, self.offsets, self.n0, self.scale,
                        self.bins.astype(dtype), self.vals.astype(dtype), self.indices, dtype,
-                       self.nthreads)
+                       self.nthreads, self.aniso)
 
     @property
     def _sfx(self):

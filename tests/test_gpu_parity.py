@@ -278,3 +278,52 @@ def test_op_without_table_and_bad_graph(gpu):
     out = C.c_double()
     assert lib.ggp_generate_logdet(h, C.byref(out), None) == 8
     assert lib.ggp_graph_destroy(h) == 0
+
+
+# ---- anisotropic covariance (src/aniso.jl) -----------------------------------------------------
+def aniso_problem(dtype):
+    z = load_fixture("aniso_parity")
+    cov = G().AnisoCov(z["spatial_bins"].astype(dtype), z["z_bins"].astype(dtype),
+                       z["grid"].astype(dtype), float(z["alpha"]))
+    prob = G().GraphGPProblem(z["coords"], z["neighbors"], z["offsets"], int(z["n0"]),
+                              float(z["scale"]), indices=z["indices"], cov=cov)
+    ref = O().Problem(prob.coords, prob.neighbors, prob.offsets, prob.n0, prob.scale,
+                      cov.spatial_bins, cov.spatial_bins, indices=prob.indices, dtype=dtype,
+                      aniso=(cov.spatial_bins, cov.z_bins, cov.grid, cov.alpha))
+    return prob, ref, z
+
+
+def test_aniso_generate_parity_fixture(gpu):
+    """Anisotropic generate / generate_inv, f64, <= 1e-11 L2 (test/python_parity_aniso.jl)."""
+    _say("case aniso_parity f64")
+    prob, ref, z = aniso_problem(np.float64)
+    hp = G().to_backend(prob)
+    f = G().generate(hp, z["xi"])
+    xi = G().generate_inv(hp, z["values"])
+    assert relerr(f, z["generate_field"]) < 1e-11
+    assert relerr(xi, z["generate_inv_xi"]) < 1e-11
+    assert relerr(G().generate_inv(hp, f), z["xi"]) < 1e-9
+    np.testing.assert_array_equal(f, ref.generate(z["xi"]))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_aniso_ops_vs_oracle(gpu, dtype):
+    _say(f"case aniso_ops {np.dtype(dtype).name}")
+    prob, ref, z = aniso_problem(dtype)
+    hp = G().to_backend(prob)
+    rng = np.random.default_rng(3)
+    xi = rng.standard_normal(prob.N).astype(dtype)
+    vb = rng.standard_normal(prob.N).astype(dtype)
+    t = tol(dtype)
+    f = G().generate(hp, xi)
+    assert relerr(f, ref.generate(xi)) < t
+    assert relerr(G().generate_inv(hp, f), ref.generate_inv(f)) < t
+    assert relerr(G().refine_logdet_terms(hp), ref.refine_logdet_terms()) < t
+    assert abs(G().generate_logdet(hp) - ref.generate_logdet()) <= t * abs(ref.generate_logdet())
+    # the transpose of the anisotropic forward map: adjoint identity (no reference result exists)
+    gx = G().generate_grad_xi(hp, vb)
+    lhs = float(np.dot(vb.astype(float), f.astype(float)))
+    rhs = float(np.dot(gx.astype(float), xi.astype(float)))
+    assert abs(lhs - rhs) <= (1e-4 if dtype == np.float32 else 1e-11) * abs(lhs)
+    with pytest.raises(G().GraphGPError):
+        G().generate_grad_vals(hp, xi, vb)
