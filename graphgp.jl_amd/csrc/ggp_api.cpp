@@ -35,7 +35,7 @@ int fail(int code, const std::string& msg) {
             return fail(GGP_ERR_HIP, std::string(#x) + ": " + hipGetErrorString(e_));         \
     } while (0)
 
-bool supported_k(int64_t k) { return k == 4 || k == 8 || k == 10 || k == 16; }
+bool supported_k(int64_t k) { return k >= 1 && k <= kMaxK; }
 bool supported_d(int64_t d) { return d >= 2 && d <= 4; }
 
 }  // namespace
@@ -144,7 +144,9 @@ int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
     const U base = Bits<T>::of(bins[1]);
     const U range = Bits<T>::of(bins[nb - 1]) - base;
     const size_t entb = (size_t)(nb - 1) * sizeof(TabEnt<T>);
-    size_t budget = h->lds_max > entb + (size_t)nb * 8 + 512 ? h->lds_max - entb - (size_t)nb * 8 - 512 : 0;
+    // slack: the kernels' static LDS (reductions, the wavefront exchange slots)
+    const size_t slack = 512 + (size_t)kWideBlock / 64 * 2 * 64 * sizeof(T);
+    size_t budget = h->lds_max > entb + (size_t)nb * 8 + slack ? h->lds_max - entb - (size_t)nb * 8 - slack : 0;
     int64_t umax = std::min<int64_t>(4096, (int64_t)(budget / 2) - 1);
     if (umax < 1) return fail(GGP_ERR_ARG, "covariance table too large for LDS");
     int shift = 0;
@@ -655,7 +657,7 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
            double scale, int32_t dtype) {
     if (!out) return fail(GGP_ERR_ARG, "null output handle");
     *out = nullptr;
-    if (!supported_k(k)) return fail(GGP_ERR_K, "unsupported k (supported: 4, 8, 10, 16)");
+    if (!supported_k(k)) return fail(GGP_ERR_K, "unsupported k (supported: 1 to 31)");
     if (!supported_d(D)) return fail(GGP_ERR_D, "unsupported D (supported: 2, 3, 4)");
     if (dtype != GGP_F32 && dtype != GGP_F64) return fail(GGP_ERR_ARG, "dtype must be GGP_F32 or GGP_F64");
     if (!(std::isfinite(scale) && scale > 0)) return fail(GGP_ERR_ARG, "scale must be finite and > 0");
@@ -710,8 +712,14 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     else h->nblk_factor = (unsigned)(h->ncu * 4);
     if (const char* e = std::getenv("GGP_PULL_BLOCKS_PER_CU")) h->nblk_pull = (unsigned)(h->ncu * std::max(1, atoi(e)));
     else h->nblk_pull = (unsigned)(h->ncu * 2);
-    h->nblk_factor = (unsigned)std::max<int64_t>(1, std::min<int64_t>(h->nblk_factor, (M + kBlock - 1) / kBlock));
-    h->nblk_pull = (unsigned)std::max<int64_t>(1, std::min<int64_t>(h->nblk_pull, (M + kBlock - 1) / kBlock));
+    // points per workgroup pass: kBlock (a lane per point) or kWideBlock/64 (a wavefront per point)
+    const int64_t ppb = register_block_k(k) ? kBlock : kWideBlock / 64;
+    if (!register_block_k(k)) {
+        if (!std::getenv("GGP_FACTOR_BLOCKS_PER_CU")) h->nblk_factor = (unsigned)(h->ncu * 8);
+        if (!std::getenv("GGP_PULL_BLOCKS_PER_CU")) h->nblk_pull = (unsigned)(h->ncu * 4);
+    }
+    h->nblk_factor = (unsigned)std::max<int64_t>(1, std::min<int64_t>(h->nblk_factor, (M + ppb - 1) / ppb));
+    h->nblk_pull = (unsigned)std::max<int64_t>(1, std::min<int64_t>(h->nblk_pull, (M + ppb - 1) / ppb));
     h->nw_dense = (int)std::max<int64_t>(1, std::min<int64_t>(h->ncu, (n0 * (n0 + 1) / 2 + kBlock - 1) / kBlock));
     Graph& g = h->g;
     g.N = N; g.n0 = n0; g.M = M; g.K = k; g.D = D; g.scale = scale;

@@ -12,16 +12,6 @@
 
 namespace ggp {
 
-__device__ inline float bcast(float x, int lane) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
-}
-__device__ inline double bcast(double x, int lane) {
-    const long long v = __double_as_longlong(x);
-    const int lo = __builtin_amdgcn_readlane((int)(v & 0xffffffffLL), lane);
-    const int hi = __builtin_amdgcn_readlane((int)(v >> 32), lane);
-    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
-}
-
 static inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ---- assembly (src/dense.jl:15-40) ----------------------------------------------------------

@@ -12,6 +12,7 @@ namespace ggp {
 
 constexpr int kBlock = 256;    // threads per workgroup of the per-point kernels
 constexpr int kTile = 32;      // dense-layer tile edge
+constexpr int kWideBlock = 256;  // threads per workgroup of the wavefront-per-point kernels
 
 // Device-resident graph (the reference's GraphGPProblem arrays after to_backend).
 struct Graph {
@@ -57,6 +58,41 @@ struct PointK {
     static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
                           int64_t q_lo, int64_t q_hi, int G, hipStream_t st);
 };
+// The same launchers for any k <= 31 (wavefront-per-point kernels, ggp_wide.h).
+template <typename T>
+struct WideK {
+    static void factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
+                       double* partial, const T* values, T* xi_out, unsigned nblk,
+                       hipStream_t st);
+    static void pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, const T* xi,
+                         const T* vb, double* hist_partial, double* scalar_partial,
+                         unsigned nblk, hipStream_t st);
+    static void sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
+                          const T* sd, int64_t m_lo, int64_t len, bool two_pass, hipStream_t st);
+    static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
+                          int64_t q_lo, int64_t q_hi, int G, hipStream_t st);
+};
+extern template struct WideK<float>;
+extern template struct WideK<double>;
+// Per-dimension factor/pullback launchers behind WideK (ggp_wide.hip, one object per (T, D)).
+template <typename T, int D>
+struct WideD {
+    static void factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
+                       double* partial, const T* values, T* xi_out, unsigned nblk,
+                       hipStream_t st);
+    static void pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, const T* xi,
+                         const T* vb, double* hist_partial, double* scalar_partial,
+                         unsigned nblk, hipStream_t st);
+};
+extern template struct WideD<float, 2>;
+extern template struct WideD<float, 3>;
+extern template struct WideD<float, 4>;
+extern template struct WideD<double, 2>;
+extern template struct WideD<double, 3>;
+extern template struct WideD<double, 4>;
+constexpr int kMaxK = 31;  // largest neighbour count (wavefront-per-point path)
+inline bool register_block_k(int64_t k) { return k == 4 || k == 8 || k == 10 || k == 16; }
+
 extern template struct PointK<float, 4>;
 extern template struct PointK<float, 8>;
 extern template struct PointK<float, 10>;

@@ -1,6 +1,6 @@
 // ggp_kernels.hip — element-wise and reduction kernels, and the (k)-dispatch to the per-point
 // kernel instantiations (ggp_point_kernels.h, compiled per (T, k) from ggp_inst.hip).
-#include "ggp_internal.h"
+#include "ggp_point_kernels.h"
 
 namespace ggp {
 
@@ -85,10 +85,63 @@ __global__ void k_copy(T* __restrict__ dst, const T* __restrict__ src, int64_t n
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) dst[i] = src[i];
 }
+// ---- the wavefront-per-point path (k not in the register-block set) ---------------------------
+template <typename T>
+void WideK<T>::factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
+                      double* partial, const T* values, T* xi_out, unsigned nblk,
+                      hipStream_t st) {
+    switch (g.D) {
+        case 2: WideD<T, 2>::factor(g, tb, mode, mv, sd, terms, partial, values, xi_out, nblk, st); break;
+        case 3: WideD<T, 3>::factor(g, tb, mode, mv, sd, terms, partial, values, xi_out, nblk, st); break;
+        case 4: WideD<T, 4>::factor(g, tb, mode, mv, sd, terms, partial, values, xi_out, nblk, st); break;
+        default: break;
+    }
+}
+
+template <typename T>
+void WideK<T>::pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, const T* xi,
+                        const T* vb, double* hist_partial, double* scalar_partial,
+                        unsigned nblk, hipStream_t st) {
+    switch (g.D) {
+        case 2: WideD<T, 2>::pullback(g, tb, mode, v, xi, vb, hist_partial, scalar_partial, nblk, st); break;
+        case 3: WideD<T, 3>::pullback(g, tb, mode, v, xi, vb, hist_partial, scalar_partial, nblk, st); break;
+        case 4: WideD<T, 4>::pullback(g, tb, mode, v, xi, vb, hist_partial, scalar_partial, nblk, st); break;
+        default: break;
+    }
+}
+
+template <typename T>
+void WideK<T>::sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
+                         const T* sd, int64_t m_lo, int64_t len, bool two_pass,
+                         hipStream_t st) {
+    if (two_pass)
+        hipLaunchKernelGGL((k_sweep_fwd<T, 0, true>), dim3(grid_for_pt(len)), dim3(kBlock), 0, st,
+                           v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len, (int)g.K);
+    else
+        hipLaunchKernelGGL((k_sweep_fwd<T, 0, false>), dim3(grid_for_pt(len)), dim3(kBlock), 0,
+                           st, v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len, (int)g.K);
+}
+
+template <typename T>
+void WideK<T>::sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
+                         int64_t q_lo, int64_t q_hi, int G, hipStream_t st) {
+    hipLaunchKernelGGL((k_sweep_rev<T, 0>), dim3(grid_for_pt((q_hi - q_lo) * G)), dim3(kBlock), 0,
+                       st, vb, vbar, xg, mv, sd, g.rev_ptr, g.rev, g.M, g.n0, q_lo, q_hi, G,
+                       (int)g.K);
+}
+
+template struct WideK<float>;
+template struct WideK<double>;
+
 // ================================ launchers ===================================================
 static inline unsigned grid_for(int64_t n, int block = kBlock) {
     return (unsigned)((n + block - 1) / block);
 }
+
+// K = 0 selects the wavefront-per-point kernels (every other k up to kMaxK).
+template <typename T, int K> struct LaunchSel { using type = PointK<T, K>; };
+template <typename T> struct LaunchSel<T, 0> { using type = WideK<T>; };
+template <typename T, int K> using Launch = typename LaunchSel<T, K>::type;
 
 #define GGP_FOR_K(CALL)                              \
     do {                                             \
@@ -97,14 +150,14 @@ static inline unsigned grid_for(int64_t n, int block = kBlock) {
             case 8: CALL(8); break;                  \
             case 10: CALL(10); break;                \
             case 16: CALL(16); break;                \
-            default: break;                          \
+            default: CALL(0); break;                 \
         }                                            \
     } while (0)
 
 template <typename T>
 void launch_factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
                    double* partial, const T* values, T* xi_out, unsigned nblk, hipStream_t st) {
-#define CALLF(KK) PointK<T, KK>::factor(g, tb, mode, mv, sd, terms, partial, values, xi_out, nblk, st)
+#define CALLF(KK) Launch<T, KK>::factor(g, tb, mode, mv, sd, terms, partial, values, xi_out, nblk, st)
     GGP_FOR_K(CALLF);
 #undef CALLF
 }
@@ -113,7 +166,7 @@ template <typename T>
 void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, const T* xi,
                      const T* vb, double* hist_partial, double* scalar_partial, unsigned nblk,
                      hipStream_t st) {
-#define CALLP(KK) PointK<T, KK>::pullback(g, tb, mode, v, xi, vb, hist_partial, scalar_partial, nblk, st)
+#define CALLP(KK) Launch<T, KK>::pullback(g, tb, mode, v, xi, vb, hist_partial, scalar_partial, nblk, st)
     GGP_FOR_K(CALLP);
 #undef CALLP
 }
@@ -121,7 +174,7 @@ void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, c
 template <typename T>
 void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
                       const T* sd, int64_t m_lo, int64_t len, bool two_pass, hipStream_t st) {
-#define CALLS(KK) PointK<T, KK>::sweep_fwd(g, v, xi, xi_off, mv, sd, m_lo, len, two_pass, st)
+#define CALLS(KK) Launch<T, KK>::sweep_fwd(g, v, xi, xi_off, mv, sd, m_lo, len, two_pass, st)
     GGP_FOR_K(CALLS);
 #undef CALLS
 }
@@ -129,7 +182,7 @@ void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T
 template <typename T>
 void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
                       int64_t q_lo, int64_t q_hi, int G, hipStream_t st) {
-#define CALLR(KK) PointK<T, KK>::sweep_rev(g, vb, vbar, xg, mv, sd, q_lo, q_hi, G, st)
+#define CALLR(KK) Launch<T, KK>::sweep_rev(g, vb, vbar, xg, mv, sd, q_lo, q_hi, G, st)
     GGP_FOR_K(CALLR);
 #undef CALLR
 }

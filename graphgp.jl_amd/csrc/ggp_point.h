@@ -36,6 +36,26 @@ template <> struct num<double> {
     __device__ static inline bits_t bits(double a) { return (bits_t)__double_as_longlong(a); }
 };
 
+// ---- cross-lane moves (wave-uniform lane index; call from wave-uniform control flow) --------
+// bcast: the value of x in `lane`, for every lane. put: x with `lane`'s value replaced by v
+// (me = the calling lane).
+__device__ inline float bcast(float x, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+__device__ inline double bcast(double x, int lane) {
+    const long long v = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_readlane((int)(v & 0xffffffffLL), lane);
+    const int hi = __builtin_amdgcn_readlane((int)(v >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+__device__ inline uint32_t bcast(uint32_t x, int lane) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, lane);
+}
+template <typename T>
+__device__ inline T put(T x, T v, int lane, int me) {
+    return me == lane ? v : x;
+}
+
 // Index of (i, j), i >= j, in a packed lower triangle.
 __host__ __device__ constexpr int tri(int i, int j) { return i * (i + 1) / 2 + j; }
 

@@ -111,16 +111,25 @@ k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, i
 // neighbour order, each product rounded before the add (that code is not under @fastmath).
 // TWO_PASS: the anisotropic apply order (src/kernels.jl:89-92): sum mv_j*v_j first, then
 // + std*xi.
+// K = 0: k is the run-time Krt (the wavefront-per-point path); otherwise Krt == K.
 template <typename T, int K, bool TWO_PASS>
 __global__ void __launch_bounds__(kBlock)
 k_sweep_fwd(T* __restrict__ v, const T* __restrict__ xi, int64_t xi_off,
             const T* __restrict__ mv, const T* __restrict__ sd, const int32_t* __restrict__ nbr,
-            int64_t M, int64_t n0, int64_t m_lo, int64_t len) {
+            int64_t M, int64_t n0, int64_t m_lo, int64_t len, int Krt) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= len) return;
     const int64_t m = m_lo + t;
-    int32_t nb[K];
-    T w[K];
+    if constexpr (K == 0) {
+        T acc = TWO_PASS ? T(0) : sd[m] * xi[xi_off + m];
+        for (int j = 0; j < Krt; ++j)
+            acc = acc + mv[(int64_t)j * M + m] * v[nbr[(int64_t)j * M + m]];
+        v[n0 + m] = TWO_PASS ? acc + sd[m] * xi[xi_off + m] : acc;
+        return;
+    }
+    constexpr int KA = K > 0 ? K : 1;
+    int32_t nb[KA];
+    T w[KA];
 #pragma unroll
     for (int j = 0; j < K; ++j) {
         nb[j] = nbr[(int64_t)j * M + m];
@@ -153,7 +162,8 @@ __global__ void __launch_bounds__(kBlock)
 k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
             const T* __restrict__ mv, const T* __restrict__ sd,
             const int64_t* __restrict__ rev_ptr, const uint32_t* __restrict__ rev,
-            int64_t M, int64_t n0, int64_t q_lo, int64_t q_hi, int G) {
+            int64_t M, int64_t n0, int64_t q_lo, int64_t q_hi, int G, int Krt) {
+    const uint32_t KK = K > 0 ? (uint32_t)K : (uint32_t)Krt;
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int lane = threadIdx.x & 63;
     const int gl = lane & (G - 1);          // lane within the group
@@ -171,7 +181,7 @@ k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
         T prod = T(0);
         if (base + gl < cnt) {
             const uint32_t c = rev[e0 + base + gl];
-            const uint32_t m = c / (uint32_t)K, j = c - m * (uint32_t)K;
+            const uint32_t m = c / KK, j = c - m * KK;
             prod = mv[(int64_t)j * M + m] * vb[n0 + m];
         }
         const int64_t take = cnt - base < G ? cnt - base : G;
@@ -369,17 +379,18 @@ void PointK<T, K>::sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, 
                              hipStream_t st) {
     if (two_pass)
         hipLaunchKernelGGL((k_sweep_fwd<T, K, true>), dim3(grid_for_pt(len)), dim3(kBlock), 0, st,
-                           v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len);
+                           v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len, (int)g.K);
     else
         hipLaunchKernelGGL((k_sweep_fwd<T, K, false>), dim3(grid_for_pt(len)), dim3(kBlock), 0,
-                           st, v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len);
+                           st, v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len, (int)g.K);
 }
 
 template <typename T, int K>
 void PointK<T, K>::sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv,
                              const T* sd, int64_t q_lo, int64_t q_hi, int G, hipStream_t st) {
     hipLaunchKernelGGL((k_sweep_rev<T, K>), dim3(grid_for_pt((q_hi - q_lo) * G)), dim3(kBlock), 0,
-                       st, vb, vbar, xg, mv, sd, g.rev_ptr, g.rev, g.M, g.n0, q_lo, q_hi, G);
+                       st, vb, vbar, xg, mv, sd, g.rev_ptr, g.rev, g.M, g.n0, q_lo, q_hi, G,
+                       (int)g.K);
 }
 
 }  // namespace ggp

@@ -46,7 +46,8 @@ def test_create_rejects_bad_inputs_before_any_device_call():
     nbr = np.ascontiguousarray(z["neighbors"], np.int64)
     offs = np.ascontiguousarray(z["offsets"], np.int64)
     n0 = int(z["n0"])
-    assert _create(coords, nbr, offs, n0, 7, 3)[0] == 2          # k unsupported
+    assert _create(coords, nbr, offs, n0, 32, 3)[0] == 2         # k above 31 unsupported
+    assert _create(coords, nbr, offs, n0, 0, 3)[0] == 2          # k = 0 unsupported
     assert _create(coords, nbr, offs, n0, 10, 5)[0] == 3         # D unsupported
     bad = offs.copy(); bad[0] += 1
     assert _create(coords, nbr, bad, n0, 10, 3)[0] == 4          # offsets[0] != n0
@@ -60,7 +61,10 @@ def test_create_rejects_bad_inputs_before_any_device_call():
     assert _create(coords, nbr, offs, n0, 10, 3, scale=-1.0)[0] == 7
     assert _create(coords, nbr, offs, n0, 10, 3, dtype=9)[0] == 7
     assert nat.hip().ggp_supported(8, 3) == 0
-    assert nat.hip().ggp_supported(9, 3) == 2
+    assert nat.hip().ggp_supported(9, 3) == 0
+    assert nat.hip().ggp_supported(31, 4) == 0
+    assert nat.hip().ggp_supported(32, 3) == 2
+    assert nat.hip().ggp_supported(8, 5) == 3
 
 
 def test_ops_require_a_device_problem():

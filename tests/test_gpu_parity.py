@@ -64,7 +64,12 @@ def tol(dtype):
 
 DTYPES = [np.float32, np.float64]
 SYNTH = [(4000, 2, 100, 4), (4000, 3, 150, 8), (3000, 3, 120, 10), (3000, 3, 200, 16),
-         (3000, 4, 150, 8)]
+         (3000, 4, 150, 8),
+         # any other k runs on the wavefront-per-point kernels (k = 5, 6, 20 as in
+         # test/test_gradients.jl:83, test/test_graph_build.jl:26, test/test_degenerate.jl:10;
+         # k = 30 as the k=30 Float64 workload; k = 1 and 31 are the ends of the range)
+         (3000, 3, 100, 5), (3000, 2, 100, 6), (2500, 3, 128, 20), (2000, 3, 120, 30),
+         (1500, 4, 100, 31), (1200, 3, 40, 1)]
 
 
 # ---------------------------------------------------------------------------------------------
@@ -105,6 +110,24 @@ def test_refine_forward_bit_exact(gpu, dtype):
     v = G().refine(hp, z["initial_values" + s], z["xi_ref" + s])
     np.testing.assert_array_equal(xi, ref.refine_inv(z["values" + s]))
     np.testing.assert_array_equal(v, ref.refine(z["initial_values" + s], z["xi_ref" + s]))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("k", [5, 20, 30])
+def test_wide_forward_bit_exact(gpu, k, dtype):
+    """The wavefront-per-point Cholesky reproduces the serial left-looking sums term by term:
+    refine_inv and refine have the oracle's bits. The logdet terms go through the device and
+    host libm log, which are not bit-identical, so they are held to the tolerance."""
+    _say(f"case wide_bit_exact k={k} {np.dtype(dtype).name}")
+    prob, ref = synth_problem(2000, 3, 100, k, dtype, seed=k)
+    hp = G().to_backend(prob)
+    rng = np.random.default_rng(k)
+    vals_tree = rng.standard_normal(prob.N).astype(dtype)
+    xr = rng.standard_normal(prob.M).astype(dtype)
+    iv = rng.standard_normal(prob.n0).astype(dtype)
+    np.testing.assert_array_equal(G().refine_inv(hp, vals_tree), ref.refine_inv(vals_tree))
+    np.testing.assert_array_equal(G().refine(hp, iv, xr), ref.refine(iv, xr))
+    assert relerr(G().refine_logdet_terms(hp), ref.refine_logdet_terms()) < tol(dtype)
 
 
 def test_generate_parity_fixture(gpu):
