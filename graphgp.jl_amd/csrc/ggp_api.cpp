@@ -61,6 +61,7 @@ struct ggp_graph {
     double* hscal = nullptr;         // pinned host mirror of dscal
     int* info = nullptr;
     int* hinfo = nullptr;            // pinned host mirror of info
+    int* dsync = nullptr;            // dense Cholesky task counter and tile flags
     double* hist = nullptr;          // (nblk_pull + nw_dense) x nb
     int hist_nb = 0;
     double *W = nullptr, *C = nullptr, *Q = nullptr, *u = nullptr;  // dense f64 scratch (lazy)
@@ -310,6 +311,7 @@ T dense_aniso_diag(const Table<T>& tb) {
 // in-op attempt reported a non-positive pivot.
 template <typename T>
 int dense_retry(ggp_graph* h) {
+    if (*h->hinfo & 2) return fail(GGP_ERR_HIP, "dense factorization: a tile wait timed out");
     const Table<T>& tb = table<T>(h);
     const int n = (int)h->g.n0;
     T dmean = T(0);
@@ -320,10 +322,11 @@ int dense_retry(ggp_graph* h) {
     while (e <= T(1e-2)) {
         launch_fill<int>(h->info, 0, 1, h->s_main);
         dense_assemble<T>(h->g, tb, tp<T>(h->A), e * dmean, h->s_main);
-        dense_potrf<T>(tp<T>(h->A), n, h->info, h->s_main);
+        dense_potrf<T>(tp<T>(h->A), n, h->info, h->dsync, std::max(1, h->ncu / 2), h->s_main);
         HC(hipMemcpyAsync(h->hinfo, h->info, sizeof(int), hipMemcpyDeviceToHost, h->s_main));
         HC(hipStreamSynchronize(h->s_main));
         if (*h->hinfo == 0) return 0;
+        if (*h->hinfo & 2) return fail(GGP_ERR_HIP, "dense factorization: a tile wait timed out");
         e *= T(10);
     }
     return fail(GGP_ERR_NOT_PD,
@@ -336,7 +339,7 @@ void dense_factor_async(ggp_graph* h, hipStream_t st) {
     tstart(h, TM_DENSE, st);
     launch_fill<int>(h->info, 0, 1, st);
     dense_assemble<T>(h->g, table<T>(h), tp<T>(h->A), T(0), st);
-    dense_potrf<T>(tp<T>(h->A), (int)h->g.n0, h->info, st);
+    dense_potrf<T>(tp<T>(h->A), (int)h->g.n0, h->info, h->dsync, std::max(1, h->ncu / 2), st);
     tstop(h, TM_DENSE, st);
 }
 
@@ -417,7 +420,6 @@ int op_generate(ggp_graph* h, const T* xi, T* out, hipStream_t user) {
     if (int rc = check_ready(h)) return rc;
     if (int rc = enter(h, user)) return rc;
     Graph& g = h->g;
-    const Table<T>& tb = table<T>(h);
     T *xt = tp<T>(h->xt), *v = tp<T>(h->v);
     launch_gather<T>(xt, xi, g.idx, g.N, h->s_main);
     if (int rc = fork(h)) return rc;
@@ -777,6 +779,7 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     rc |= dmalloc(h, (void**)&h->scal_partial, std::max(h->nblk_factor, h->nblk_pull) * 8);
     rc |= dmalloc(h, (void**)&h->dscal, 8 * 8);
     rc |= dmalloc(h, (void**)&h->info, 16);
+    rc |= dmalloc(h, (void**)&h->dsync, (size_t)dense_sync_ints((int)n0) * sizeof(int));
     if (rc) return bail(GGP_ERR_HIP);
     if (hipHostMalloc((void**)&h->hscal, 8 * 8) != hipSuccess ||
         hipHostMalloc((void**)&h->hinfo, 16) != hipSuccess)

@@ -39,133 +39,176 @@ __global__ void k_dense_assemble(T* __restrict__ A, const uint32_t* __restrict__
     A[(int64_t)j * n + i] = v;
 }
 
-// ---- blocked Cholesky -------------------------------------------------------------------------
-// Panel step kb (block column of kTile columns).
-//  1. Wave 0 of every workgroup factors the diagonal tile right-looking: lane r owns row r in
-//     registers; the pivot of column p comes from lane p by readlane, and the column's entries
-//     are broadcast through LDS (one wave: no block barrier, only a wave-level code-motion fence).
-//     Entry (r, c) receives fma(-L[r][p], L[c][p], .) for p = 0, 1, ... in order — the same fma
-//     chain as the left-looking recurrence. Workgroup 0 writes the tile back and raises *info on
-//     a non-positive pivot (LAPACK potrf's failure condition, src/dense.jl:47-48).
-//  2. After one block barrier every thread solves one row below the tile left-looking against
-//     the factored tile in LDS: (a_jj - sum_{p<jj} a_p L[jj][p]) / L[jj][jj].
-constexpr int kPanelThreads = 256;
-constexpr int kLStride = kTile + 4;  // LDS row stride: rows stay 16-byte aligned for b128 reads
+// ---- tiled Cholesky: one persistent launch ----------------------------------------------------
+// The lower triangle is cut into 32x32 tiles (i, j), i >= j. Every tile is one task:
+//   1. its entries receive fma(-L[r][p], L[c][p], .) for p = 0, 1, ... over the finished tiles
+//      (i, k) and (j, k), k < j, in increasing k (streamed: each k-tile is applied as soon as its
+//      two inputs are published);
+//   2. a diagonal tile is then factored right-looking by one wavefront (lane r owns row r; the
+//      pivot and the column come from their lanes by readlane), an off-diagonal tile solved row
+//      by row against the published L[j][j].
+// Entry (r, c) thus receives exactly the fma chain of the unblocked left-looking recurrence, in
+// the same order, and the factor is bit-identical to it. LAPACK potrf's failure condition (a
+// non-positive pivot, src/dense.jl:47-48) sets bit 0 of *info.
+//
+// Scheduling: workgroups take tasks from an atomic ticket counter in column-major tile order,
+// which is a topological order of the task graph, so a task only ever waits for tasks already
+// taken by running workgroups and the launch cannot deadlock, whatever the residency. A finished
+// tile is published with a release store of its flag after its stores; consumers acquire the
+// flag. Every wait is bounded: past kDfSpinLimit polls the waiter sets bit 1 of *info and goes
+// on, so every workgroup exits; the host reports that as an error.
+constexpr int kDfThreads = 256;
+constexpr int kDfSpinLimit = 1 << 20;  // polls: about a second at most
 
-// FULL: the block column has all kTile columns (every panel but possibly the last), so the
-// loops carry no bounds checks.
-template <typename T, bool FULL>
-__global__ void __launch_bounds__(kPanelThreads) k_potrf_panel(T* __restrict__ A, int n, int kb,
-                                                               int* __restrict__ info) {
-    __shared__ __align__(16) T sL[kTile * kLStride];
-    __shared__ __align__(16) T scol[kTile];
+// Poll with relaxed loads (no cache invalidation per poll), then one acquire fence.
+__device__ inline void df_wait(const int* flag, int* info) {
+    int spins = 0;
+    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > kDfSpinLimit) {
+            atomicOr(info, 2);
+            break;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// sync = [ticket, flags[nt * nt]] (zeroed before the launch).
+template <typename T>
+__global__ void __launch_bounds__(kDfThreads) k_potrf_tiles(T* __restrict__ A, int n, int nt,
+                                                            int* __restrict__ sync,
+                                                            int* __restrict__ info) {
+    __shared__ T sA[kTile][kTile + 1];
+    __shared__ T sB[kTile][kTile + 1];
+    __shared__ int s_task;
+    int* ticket = sync;
+    int* flags = sync + 1;
     const int tid = threadIdx.x;
-    const int k0 = kb * kTile;
-    const int nk = FULL ? kTile : min(kTile, n - k0);
-    if (tid < 64) {
-        // Entries above the diagonal are scratch: they receive harmless updates and are
-        // never read back, which keeps every update unconditional.
-        const int r = tid;
-        T a[kTile];
-        const T* rp = A + (int64_t)(k0 + (r < nk ? r : 0)) * n + k0;
+    const int c = tid & (kTile - 1), r0 = tid >> 5;  // entries (r0 + 8q, c), q = 0..3
+    const int ntiles = nt * (nt + 1) / 2;
+    // The loop test is on a workgroup-uniform value the compiler can see as uniform
+    // (readfirstlane), and the single-thread work (publish, next ticket) sits mid-body between
+    // barriers: a lane-divergent branch at the loop head or latch lets the compiler split the
+    // loop, which separates the flag store from the task it publishes.
+    if (tid == 0) s_task = atomicAdd(ticket, 1);
+    __syncthreads();
+    int t = __builtin_amdgcn_readfirstlane(s_task);
+    while (t < ntiles) {
+        __syncthreads();
+        int j = 0, rem = t;
+        while (rem >= nt - j) { rem -= nt - j; ++j; }
+        const int i = j + rem;
+        const int i0 = i * kTile, j0 = j * kTile;
+        const bool diag = i == j;
+        // Rows and columns past n are padding: zero, with a unit diagonal, so they stay finite
+        // and never feed a real entry (L is lower triangular).
+        T acc[4];
 #pragma unroll
-        for (int c = 0; c < kTile; ++c) a[c] = (r < nk && (FULL || c < nk)) ? rp[c] : T(0);
-        bool bad = false;
+        for (int q = 0; q < 4; ++q) {
+            const int r = r0 + 8 * q;
+            acc[q] = (i0 + r < n && j0 + c < n) ? A[(int64_t)(i0 + r) * n + j0 + c]
+                                                : (diag && r == c ? T(1) : T(0));
+        }
+        for (int k = 0; k < j; ++k) {
+            if (tid == 0) {
+                df_wait(&flags[i * nt + k], info);
+                if (!diag) df_wait(&flags[j * nt + k], info);
+            }
+            __syncthreads();
+            const int k0 = k * kTile;
 #pragma unroll
-        for (int p = 0; p < kTile; ++p) {
-            if (FULL || p < nk) {
-                const T piv = bcast(a[p], p);
-                bad = bad || !(piv > T(0));
-                const T d = num<T>::sqrt(piv);
-                const T l = a[p] / d;
-                a[p] = r == p ? d : l;
-                if (r < kTile) scol[r] = a[p];
-                __builtin_amdgcn_wave_barrier();
+            for (int q = 0; q < 4; ++q) {
+                const int r = r0 + 8 * q;
+                sA[r][c] = i0 + r < n ? A[(int64_t)(i0 + r) * n + k0 + c] : T(0);
+                sB[r][c] = j0 + r < n ? A[(int64_t)(j0 + r) * n + k0 + c] : T(0);
+            }
+            __syncthreads();
+#pragma unroll 8
+            for (int p = 0; p < kTile; ++p) {
+                const T lc = sB[c][p];
 #pragma unroll
-                for (int c = p + 1; c < kTile; ++c) a[c] = num<T>::fma(-a[p], scol[c], a[c]);
-                __builtin_amdgcn_wave_barrier();
+                for (int q = 0; q < 4; ++q) acc[q] = num<T>::fma(-sA[r0 + 8 * q][p], lc, acc[q]);
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sA[r0 + 8 * q][c] = acc[q];
+        if (!diag) {
+            if (tid == 0) df_wait(&flags[j * nt + j], info);
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = r0 + 8 * q;
+                sB[r][c] = (j0 + r < n && c <= r) ? A[(int64_t)(j0 + r) * n + j0 + c] : T(0);
             }
         }
-        if (r < nk) {
+        __syncthreads();
+        if (tid < 64) {
+            const int r = tid & (kTile - 1);
+            const bool live = tid < kTile && i0 + r < n;
+            T a[kTile];
 #pragma unroll
-            for (int c = 0; c < kTile; ++c) sL[r * kLStride + c] = a[c];
-            if (blockIdx.x == 0) {
-                T* wp = A + (int64_t)(k0 + r) * n + k0;
+            for (int cc = 0; cc < kTile; ++cc) a[cc] = sA[r][cc];
+            if (diag) {
+                // Entries above the diagonal are scratch: they take harmless updates and are
+                // never stored, which keeps every update unconditional.
+                bool bad = false;
 #pragma unroll
-                for (int c = 0; c < kTile; ++c)
-                    if (c <= r && (FULL || c < nk)) wp[c] = a[c];
+                for (int p = 0; p < kTile; ++p) {
+                    const T piv = bcast(a[p], p);
+                    bad = bad || !(piv > T(0));
+                    const T d = num<T>::sqrt(piv);
+                    const T l = a[p] / d;
+                    a[p] = r == p ? d : l;
+#pragma unroll
+                    for (int cc = p + 1; cc < kTile; ++cc)
+                        a[cc] = num<T>::fma(-a[p], bcast(a[p], cc), a[cc]);
+                }
+                if (live) {
+                    T* wp = A + (int64_t)(i0 + r) * n + j0;
+#pragma unroll
+                    for (int cc = 0; cc < kTile; ++cc)
+                        if (cc <= r) wp[cc] = a[cc];
+                }
+                if (tid == 0 && bad) atomicOr(info, 1);
+            } else {
+#pragma unroll
+                for (int jj = 0; jj < kTile; ++jj) {
+                    T tt = a[jj];
+#pragma unroll
+                    for (int p = 0; p < jj; ++p) tt = num<T>::fma(-a[p], sB[jj][p], tt);
+                    a[jj] = tt / sB[jj][jj];
+                }
+                if (live) {
+                    T* wp = A + (int64_t)(i0 + r) * n + j0;
+#pragma unroll
+                    for (int cc = 0; cc < kTile; ++cc) wp[cc] = a[cc];
+                }
             }
         }
-        if (blockIdx.x == 0 && r == 0 && bad) atomicOr(info, 1);
-    }
-    __syncthreads();
-    const int row = k0 + kTile + (int)blockIdx.x * kPanelThreads + tid;
-    if (row >= n) return;
-    T b[kTile];
-    T* rp = A + (int64_t)row * n + k0;
-#pragma unroll
-    for (int c = 0; c < kTile; ++c) b[c] = (FULL || c < nk) ? rp[c] : T(0);
-#pragma unroll
-    for (int jj = 0; jj < kTile; ++jj) {
-        if (FULL || jj < nk) {
-            const T* lrow = sL + jj * kLStride;
-            T t = b[jj];
-#pragma unroll
-            for (int p = 0; p < jj; ++p) t = num<T>::fma(-b[p], lrow[p], t);
-            b[jj] = t / lrow[jj];
+        __syncthreads();
+        if (tid == 0) {
+            __hip_atomic_store(&flags[i * nt + j], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            s_task = atomicAdd(ticket, 1);
         }
-    }
-#pragma unroll
-    for (int c = 0; c < kTile; ++c)
-        if (FULL || c < nk) rp[c] = b[c];
-}
-
-// Trailing update after panel kb: tile (ib, jb), kb < jb <= ib, gets
-// a = fma(-L[i][p], L[j][p], a) for the panel columns p in order.
-template <typename T>
-__global__ void __launch_bounds__(256) k_potrf_update(T* __restrict__ A, int n, int kb) {
-    __shared__ T Pi[kTile][kTile + 1];
-    __shared__ T Pj[kTile][kTile + 1];
-    const int t = blockIdx.x;
-    int ti = (int)((sqrt(8.0 * t + 1.0) - 1.0) * 0.5);
-    while ((ti + 1) * (ti + 2) / 2 <= t) ++ti;
-    while (ti * (ti + 1) / 2 > t) --ti;
-    const int tj = t - ti * (ti + 1) / 2;
-    const int ib = kb + 1 + ti, jb = kb + 1 + tj;
-    const int k0 = kb * kTile, nk = min(kTile, n - k0);
-    const int i0 = ib * kTile, j0 = jb * kTile;
-    const int ni = min(kTile, n - i0), nj = min(kTile, n - j0);
-    for (int e = threadIdx.x; e < kTile * kTile; e += blockDim.x) {
-        const int r = e / kTile, c = e % kTile;
-        Pi[r][c] = (r < ni && c < nk) ? A[(int64_t)(i0 + r) * n + k0 + c] : T(0);
-        Pj[r][c] = (r < nj && c < nk) ? A[(int64_t)(j0 + r) * n + k0 + c] : T(0);
-    }
-    __syncthreads();
-    const int tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;
-    for (int r = ty; r < ni; r += blockDim.x / kTile) {
-        const int c = tx;
-        if (c >= nj || (ib == jb && c > r)) continue;
-        T* p = A + (int64_t)(i0 + r) * n + j0 + c;
-        T v = *p;
-        for (int q = 0; q < nk; ++q) v = num<T>::fma(-Pi[r][q], Pj[c][q], v);
-        *p = v;
+        __syncthreads();
+        t = __builtin_amdgcn_readfirstlane(s_task);
     }
 }
 
-template <typename T>
-void dense_potrf(T* A, int n, int* info, hipStream_t st) {
+int dense_sync_ints(int n) {
     const int nt = (n + kTile - 1) / kTile;
-    for (int kb = 0; kb < nt; ++kb) {
-        const int below = n - kb * kTile - kTile;
-        const unsigned nblk = below > 0 ? (unsigned)((below + kPanelThreads - 1) / kPanelThreads) : 1u;
-        if (n - kb * kTile >= kTile)
-            hipLaunchKernelGGL((k_potrf_panel<T, true>), dim3(nblk), dim3(kPanelThreads), 0, st, A, n, kb, info);
-        else
-            hipLaunchKernelGGL((k_potrf_panel<T, false>), dim3(nblk), dim3(kPanelThreads), 0, st, A, n, kb, info);
-        const int m = nt - kb - 1;
-        if (m > 0)
-            hipLaunchKernelGGL((k_potrf_update<T>), dim3(m * (m + 1) / 2), dim3(256), 0, st, A, n, kb);
-    }
+    return nt * nt + 1;
+}
+
+template <typename T>
+void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st) {
+    if (n <= 0) return;
+    const int nt = (n + kTile - 1) / kTile;
+    const int ntiles = nt * (nt + 1) / 2;
+    launch_fill<int>(sync, 0, dense_sync_ints(n), st);
+    const int nwg = std::max(1, std::min(ntiles, max_wg));
+    hipLaunchKernelGGL((k_potrf_tiles<T>), dim3(nwg), dim3(kDfThreads), 0, st, A, n, nt, sync, info);
 }
 
 // ---- triangular products and solves ---------------------------------------------------------
@@ -578,7 +621,7 @@ void dense_grad_invloss(const Graph& g, const Table<T>& tb, const T* alpha, doub
 
 #define GGP_DENSE_INST(T)                                                                      \
     template void dense_assemble<T>(const Graph&, const Table<T>&, T*, T, hipStream_t);        \
-    template void dense_potrf<T>(T*, int, int*, hipStream_t);                                  \
+    template void dense_potrf<T>(T*, int, int*, int*, int, hipStream_t);                                  \
     template void dense_trmv<T>(const T*, int, const T*, T*, hipStream_t);                     \
     template void dense_trmv_t<T>(const T*, int, const T*, T*, hipStream_t);                   \
     template void dense_trsv<T>(const T*, int, const T*, T*, hipStream_t);                     \

@@ -135,8 +135,12 @@ void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st);
 // Dense first layer (ggp_dense.hip). Matrices are n x n row-major; L lower.
 template <typename T>
 void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStream_t st);
+// Cholesky in place (lower), one persistent launch of at most max_wg workgroups; sync is a
+// workspace of dense_sync_ints(n) ints. *info: bit 0 = non-positive pivot, bit 1 = a wait ran
+// past its bound (the result is then invalid).
 template <typename T>
-void dense_potrf(T* A, int n, int* info, hipStream_t st);
+void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st);
+int dense_sync_ints(int n);
 template <typename T>
 void dense_trmv(const T* L, int n, const T* x, T* y, hipStream_t st);
 template <typename T>
