@@ -362,9 +362,6 @@ void pullback_t(ggp_graph* h, int mode, const T* v, const T* xi, const T* vb) {
 
 int ensure_dense64(ggp_graph* h) {
     if (h->W) return 0;
-    // the inverse kernel keeps one column of L^-1 (n0 doubles) in LDS
-    if ((size_t)h->g.n0 * sizeof(double) > h->lds_max)
-        return fail(GGP_ERR_ARG, "dense-layer gradients support n0 up to lds/8 (8192)");
     const size_t nn = (size_t)h->g.n0 * (size_t)h->g.n0 * sizeof(double);
     if (dmalloc(h, (void**)&h->W, nn) || dmalloc(h, (void**)&h->C, nn) ||
         dmalloc(h, (void**)&h->Q, nn) || dmalloc(h, (void**)&h->u, (size_t)h->g.n0 * 8))

@@ -8,6 +8,8 @@
 // Cholesky adjoint, Abar = L^-T Phi(L^T Lbar) L^-1 (Phi = lower triangle, halved diagonal),
 // instead of the reference's scalar reverse sweep (src/grad_generate_vals.jl:18-39), which is
 // the same derivative evaluated in a parallel order.
+#include <algorithm>
+
 #include "ggp_internal.h"
 
 namespace ggp {
@@ -352,119 +354,207 @@ void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStr
 }
 
 // ---- dense cotangents (f64) -----------------------------------------------------------------
-// W = L^-1 in double. One wave solves kInvCols consecutive columns c0.. (so each row of L it reads
-// serves all of them), left-looking over 64-row blocks: lane l of block r0 first forms
-// acc_c = e_c[r] - sum_{c0<=p<r0} L[r][p] x_c[p] along its own row r = r0+l of L (contiguous
-// reads; x in LDS), then the 64 x 64 diagonal block is solved from registers with the pivots
-// broadcast by readlane.
-constexpr int kInvCols = 1;
+// ---- f64 matrix-core GEMM ---------------------------------------------------------------------
+// C = alpha * op(A) * B for a batch of independent jobs, on v_mfma_f64_16x16x4f64. Each
+// workgroup owns a 64x64 tile of one job's C; its four wavefronts own 32x32 quarters (2 x 2
+// MFMA blocks). k advances in 32-deep chunks staged in LDS, the next chunk prefetched into
+// registers while the current one is multiplied. Operand layout of the instruction: A[i][k] in
+// lane i + 16k, B[k][j] in lane j + 16k; D[i][j] in lane j + 16(i mod 4), element i / 4.
+//
+// Triangular operands: flags restrict k to the part that can be non-zero for the tile
+// (GK_FROM_I: k >= i0, GK_FROM_J: k >= j0, GK_TO_I: k < i0 + 64); entries the flags skip are zero
+// in the operand, so the product is unchanged. GK_LOWER skips tiles strictly above the diagonal.
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+constexpr int kGM = 64, kGK = 32, kGemmJobs = 24;
+enum GemmFlags { GK_FROM_I = 1, GK_FROM_J = 2, GK_TO_I = 4, GK_LOWER = 8 };
+struct GemmJob {
+    const void* A;
+    const double* B;
+    double* C;
+    int lda, ldb, ldc;
+    int M, N, K;
+    int atrans;  // op(A)(i, k) = A[k*lda + i] when set, A[i*lda + k] otherwise
+    int flags;
+    int tiles_n, tile0;
+    double alpha;
+};
+struct GemmBatch {
+    GemmJob job[kGemmJobs];
+    int njobs;
+};
 
-// lr[lane] of a 64-entry register row, selected by the lane's own index (a select chain, since
-// registers cannot be indexed at run time).
-__device__ inline double bcast_lane_diag(const double (&lr)[64], int lane) {
-    double v = 1.0;
+template <typename TA>
+__global__ void __launch_bounds__(256) k_gemm64(GemmBatch batch) {
+    __shared__ double sA[kGK][kGM + 2];
+    __shared__ double sB[kGK][kGM + 2];
+    int jb = 0;
+    while (jb + 1 < batch.njobs && batch.job[jb + 1].tile0 <= (int)blockIdx.x) ++jb;
+    const GemmJob& g = batch.job[jb];
+    const int t = (int)blockIdx.x - g.tile0;
+    const int i0 = (t / g.tiles_n) * kGM, j0 = (t % g.tiles_n) * kGM;
+    if ((g.flags & GK_LOWER) && j0 > i0) return;
+    int ks = 0, ke = g.K;
+    if (g.flags & GK_FROM_I) ks = max(ks, i0);
+    if (g.flags & GK_FROM_J) ks = max(ks, j0);
+    if (g.flags & GK_TO_I) ke = min(ke, i0 + kGM);
+    ks = (ks / kGK) * kGK;
+    const TA* __restrict__ A = static_cast<const TA*>(g.A);
+    const double* __restrict__ B = g.B;
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
+    const int wr = (w >> 1) * 32, wc = (w & 1) * 32;
+    f64x4 acc[2][2];
 #pragma unroll
-    for (int jj = 0; jj < 64; ++jj) v = lane == jj ? lr[jj] : v;
-    return v;
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = (f64x4){0.0, 0.0, 0.0, 0.0};
+    // register staging of one chunk: 8 A and 8 B entries per thread
+    double ra[8], rb[8];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int e = tid + 256 * q;
+            int ii, kk;
+            if (g.atrans) { kk = e / kGM; ii = e % kGM; } else { ii = e / kGK; kk = e % kGK; }
+            const int gi = i0 + ii, gk = k0 + kk;
+            ra[q] = (gi < g.M && gk < ke)
+                        ? (double)(g.atrans ? A[(int64_t)gk * g.lda + gi] : A[(int64_t)gi * g.lda + gk])
+                        : 0.0;
+            const int kb = e / kGM, jj = e % kGM;
+            const int gj = j0 + jj, gkb = k0 + kb;
+            rb[q] = (gj < g.N && gkb < ke) ? B[(int64_t)gkb * g.ldb + gj] : 0.0;
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int e = tid + 256 * q;
+            int ii, kk;
+            if (g.atrans) { kk = e / kGM; ii = e % kGM; } else { ii = e / kGK; kk = e % kGK; }
+            sA[kk][ii] = ra[q];
+            sB[e / kGM][e % kGM] = rb[q];
+        }
+    };
+    if (ks < ke) fetch(ks);
+    for (int k0 = ks; k0 < ke; k0 += kGK) {
+        __syncthreads();
+        stash();
+        __syncthreads();
+        if (k0 + kGK < ke) fetch(k0 + kGK);
+#pragma unroll
+        for (int s = 0; s < kGK / 4; ++s) {
+            const int kr = s * 4 + (l >> 4);
+            const double a0 = sA[kr][wr + (l & 15)], a1 = sA[kr][wr + 16 + (l & 15)];
+            const double b0 = sB[kr][wc + (l & 15)], b1 = sB[kr][wc + 16 + (l & 15)];
+            acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int i = i0 + wr + 16 * a + (l >> 4) + 4 * v;
+                const int j = j0 + wc + 16 * b + (l & 15);
+                if (i < g.M && j < g.N) g.C[(int64_t)i * g.ldc + j] = g.alpha * acc[a][b][v];
+            }
+}
+
+// Launch a list of jobs (split into batches of kGemmJobs).
+template <typename TA>
+static void launch_gemm(std::vector<GemmJob> jobs, hipStream_t st) {
+    for (size_t s = 0; s < jobs.size(); s += kGemmJobs) {
+        GemmBatch b{};
+        int tiles = 0;
+        b.njobs = (int)std::min<size_t>(kGemmJobs, jobs.size() - s);
+        for (int q = 0; q < b.njobs; ++q) {
+            GemmJob j = jobs[s + q];
+            j.tiles_n = (j.N + kGM - 1) / kGM;
+            j.tile0 = tiles;
+            tiles += ((j.M + kGM - 1) / kGM) * j.tiles_n;
+            b.job[q] = j;
+        }
+        if (tiles > 0) hipLaunchKernelGGL((k_gemm64<TA>), dim3(tiles), dim3(256), 0, st, b);
+    }
+}
+
+static GemmJob gemm_job(const void* A, int lda, int atrans, const double* B, int ldb, double* C,
+                        int ldc, int M, int N, int K, int flags, double alpha) {
+    GemmJob j{};
+    j.A = A; j.lda = lda; j.atrans = atrans;
+    j.B = B; j.ldb = ldb;
+    j.C = C; j.ldc = ldc;
+    j.M = M; j.N = N; j.K = K;
+    j.flags = flags;
+    j.alpha = alpha;
+    return j;
+}
+
+// ---- W = L^-1 (f64) ---------------------------------------------------------------------------
+// Diagonal 32x32 blocks are inverted directly (one column per lane, forward substitution); then
+// the off-diagonal blocks follow from the 2x2 block identity
+//   [A 0; B C]^-1 = [A^-1 0; -C^-1 B A^-1  C^-1],
+// applied recursively (splits on 32-row boundaries): every recursion level is one batched GEMM
+// T = B A^-1 followed by one batched GEMM X = -C^-1 T, the nodes of a level being independent.
+template <typename T>
+__global__ void __launch_bounds__(64) k_trinv_leaf(const T* __restrict__ L, int n,
+                                                   double* __restrict__ W) {
+    __shared__ double sL[32][33];
+    const int o = blockIdx.x * 32, tid = threadIdx.x;
+    const int nb = min(32, n - o);
+    for (int e = tid; e < 32 * 32; e += 64) {
+        const int r = e / 32, c = e % 32;
+        sL[r][c] = (r < nb && c <= r) ? (double)L[(int64_t)(o + r) * n + o + c] : (r == c ? 1.0 : 0.0);
+    }
+    __syncthreads();
+    if (tid >= 32) return;
+    const int c = tid;
+    double w[32];
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+        double s = r == c ? 1.0 : 0.0;
+#pragma unroll
+        for (int k = 0; k < r; ++k) s = __builtin_fma(-sL[r][k], w[k], s);
+        w[r] = r >= c ? s / sL[r][r] : 0.0;
+    }
+    if (c < nb)
+#pragma unroll
+        for (int r = 0; r < 32; ++r)
+            if (r < nb) W[(int64_t)(o + r) * n + o + c] = w[r];
+}
+
+// Recursion plan: jobs[depth] = {first GEMMs, second GEMMs} of the nodes at that depth.
+template <typename T>
+static void trinv_plan(const T* L, double* W, double* S, int n, int o, int sz, int depth,
+                       std::vector<std::vector<GemmJob>>& g1, std::vector<std::vector<GemmJob>>& g2) {
+    if (sz <= 32) return;
+    const int nb = (sz + 31) / 32;
+    const int m = 32 * ((nb + 1) / 2), s2 = sz - m;
+    trinv_plan(L, W, S, n, o, m, depth + 1, g1, g2);
+    trinv_plan(L, W, S, n, o + m, s2, depth + 1, g1, g2);
+    if ((int)g1.size() <= depth) { g1.resize(depth + 1); g2.resize(depth + 1); }
+    const int64_t off = (int64_t)(o + m) * n + o;
+    // T = B A^-1: B = L[o+m.., o..] (s2 x m), A^-1 = W[o.., o..] lower (k >= column)
+    g1[depth].push_back(gemm_job(L + off, n, 0, W + (int64_t)o * n + o, n, S + off, n, s2, m, m,
+                                 GK_FROM_J, 1.0));
+    // X = -C^-1 T: C^-1 = W[o+m.., o+m..] lower (k <= row)
+    g2[depth].push_back(gemm_job(W + (int64_t)(o + m) * n + o + m, n, 0, S + off, n, W + off, n,
+                                 s2, m, s2, GK_TO_I, -1.0));
 }
 
 template <typename T>
-__global__ void __launch_bounds__(64) k_trinv(const T* __restrict__ L, int n,
-                                              double* __restrict__ W) {
-    extern __shared__ double sx[];  // kInvCols x n
-    const int c0 = blockIdx.x * kInvCols, lane = threadIdx.x;
-    for (int r0 = c0; r0 < n; r0 += 64) {
-        const int r = r0 + lane;
-        const bool live = r < n;
-        const T* row = L + (int64_t)(live ? r : 0) * n;
-        double acc[kInvCols];
-#pragma unroll
-        for (int q = 0; q < kInvCols; ++q) acc[q] = (r == c0 + q) ? 1.0 : 0.0;
-        if (live) {
-#pragma unroll 4
-            for (int p = c0; p < r0; ++p) {
-                const double lp = (double)row[p];
-#pragma unroll
-                for (int q = 0; q < kInvCols; ++q) acc[q] = __builtin_fma(-lp, sx[q * n + p], acc[q]);
-            }
-        }
-        double lr[64];
-#pragma unroll
-        for (int jj = 0; jj < 64; ++jj) lr[jj] = (live && r0 + jj < n) ? (double)row[r0 + jj] : 1.0;
-        // one reciprocal per row: lane l holds 1 / L[r0+l][r0+l]
-        const double rinv = 1.0 / bcast_lane_diag(lr, lane);
-#pragma unroll
-        for (int jj = 0; jj < 64; ++jj) {
-            if (r0 + jj < n) {
-                const double rp = bcast(rinv, jj);
-#pragma unroll
-                for (int q = 0; q < kInvCols; ++q) {
-                    const double xj = bcast(acc[q], jj) * rp;
-                    if (lane == jj) acc[q] = xj;
-                    else if (lane > jj) acc[q] = __builtin_fma(-lr[jj], xj, acc[q]);
-                }
-            }
-        }
-        if (live)
-#pragma unroll
-            for (int q = 0; q < kInvCols; ++q) sx[q * n + r] = acc[q];
-        __syncthreads();
+static void dense_inverse64(const T* L, int n, double* W, double* S, hipStream_t st) {
+    launch_fill<double>(W, 0.0, (int64_t)n * n, st);
+    hipLaunchKernelGGL((k_trinv_leaf<T>), dim3(cdiv(n, 32)), dim3(64), 0, st, L, n, W);
+    std::vector<std::vector<GemmJob>> g1, g2;
+    trinv_plan<T>(L, W, S, n, 0, n, 0, g1, g2);
+    for (int d = (int)g1.size() - 1; d >= 0; --d) {
+        launch_gemm<T>(g1[d], st);
+        launch_gemm<double>(g2[d], st);
     }
-    for (int q = 0; q < kInvCols; ++q) {
-        const int c = c0 + q;
-        if (c >= n) break;
-        for (int r = lane; r < n; r += 64) W[(int64_t)r * n + c] = r < c ? 0.0 : sx[q * n + r];
-    }
-}
-
-// C[i][j] = sum_{a >= max(i, j)} W[a][i] X[a][j] for lower-triangular W, X (n x n, row-major):
-// 64 x 64 output tiles, 4 x 4 outputs per thread, 16-row slabs of W and X staged in LDS.
-// lower_only: only tiles with i >= j.
-constexpr int kWT = 64, kWK = 16;
-__global__ void __launch_bounds__(256) k_wtx(const double* __restrict__ W,
-                                             const double* __restrict__ X, int n,
-                                             double* __restrict__ C, int lower_only) {
-    __shared__ double sW[kWK][kWT + 1];
-    __shared__ double sX[kWK][kWT + 1];
-    const int bi = blockIdx.y, bj = blockIdx.x;
-    if (lower_only && bj > bi) return;
-    const int i0 = bi * kWT, j0 = bj * kWT;
-    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-    double acc[4][4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[u][v] = 0.0;
-    const int a_start = (max(i0, j0) / kWK) * kWK;
-    for (int a0 = a_start; a0 < n; a0 += kWK) {
-        for (int e = threadIdx.x; e < kWK * kWT; e += blockDim.x) {
-            const int rr = e / kWT, cc = e % kWT;
-            const int a = a0 + rr;
-            sW[rr][cc] = (a < n && i0 + cc < n) ? W[(int64_t)a * n + i0 + cc] : 0.0;
-            sX[rr][cc] = (a < n && j0 + cc < n) ? X[(int64_t)a * n + j0 + cc] : 0.0;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int rr = 0; rr < kWK; ++rr) {
-            double w[4], x[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) w[u] = sW[rr][ty + 16 * u];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) x[v] = sX[rr][tx + 16 * v];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc[u][v] = __builtin_fma(w[u], x[v], acc[u][v]);
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int i = i0 + ty + 16 * u, j = j0 + tx + 16 * v;
-            if (i < n && j < n) C[(int64_t)i * n + j] = acc[u][v];
-        }
 }
 
 // u = L^T vb (double), h/Q prefix pass: Q[a][j] = u[a] (sum_{j<=b<a} xi[b] W[b][j] + xi[a]W[a][j]/2)
@@ -579,20 +669,14 @@ static void launch_dense_scatter(const Graph& g, const Table<T>& tb, const doubl
     }
 }
 
-template <typename T>
-static void dense_inverse64(const T* L, int n, double* W, double* /*scratch*/, hipStream_t st) {
-    hipLaunchKernelGGL((k_trinv<T>), dim3(cdiv(n, kInvCols)), dim3(64),
-                       (size_t)kInvCols * n * sizeof(double), st, L, n, W);
-}
 
 // d(sum log diag L)/dvals: Kinv = W^T W, diagonal halved (src/dense.jl:153-183).
 template <typename T>
 void dense_grad_logdet(const Graph& g, const Table<T>& tb, const T* L, double* W, double* C,
                        double* hist_partial, int nw, hipStream_t st) {
     const int n = (int)g.n0;
-    dense_inverse64(L, n, W, C, st);  // C doubles as the L^T scratch
-    const dim3 grid(cdiv(n, kWT), cdiv(n, kWT));
-    hipLaunchKernelGGL(k_wtx, grid, dim3(256), 0, st, W, W, n, C, 1);
+    dense_inverse64(L, n, W, C, st);  // C is the inversion's scratch, then K^-1 (lower)
+    launch_gemm<double>({gemm_job(W, n, 1, W, n, C, n, n, n, n, GK_FROM_I | GK_FROM_J | GK_LOWER, 1.0)}, st);
     launch_dense_scatter<T, DM_LOGDET>(g, tb, C, nullptr, hist_partial, nw, st);
 }
 
@@ -607,8 +691,7 @@ void dense_grad_generate(const Graph& g, const Table<T>& tb, const T* L, const T
     dense_inverse64(L, n, W, C, st);
     hipLaunchKernelGGL((k_ltv64<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, L, n, vb, u);
     hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 32)), dim3(256), 0, st, W, n, xi, u, Q);
-    const dim3 grid(cdiv(n, kWT), cdiv(n, kWT));
-    hipLaunchKernelGGL(k_wtx, grid, dim3(256), 0, st, W, Q, n, C, 0);
+    launch_gemm<double>({gemm_job(W, n, 1, Q, n, C, n, n, n, n, GK_FROM_I | GK_FROM_J, 1.0)}, st);
     launch_dense_scatter<T, DM_GENERATE>(g, tb, C, nullptr, hist_partial, nw, st);
 }
 
