@@ -95,8 +95,19 @@ def hip():
             raise RuntimeError(
                 f"libgraphgp_hip.so not found at {HIP_LIB}: build it first "
                 "(python -c 'import __graft_entry__ as g; g.build()' or make -C graphgp.jl_amd/csrc)")
+        _torch_runtime_first()
         _hip = _bind(HIP_LIB, _HIP_SIGS)
     return _hip
+
+
+def _torch_runtime_first():
+    """Load torch's HIP runtime before the library. Both provide libamdhip64.so.7; loaded
+    first, torch's copy satisfies the library's dependency and the process has one runtime.
+    Loaded the other way round the process ends up with two, and torch then sees no GPU."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
 
 
 def graphlib():

@@ -56,6 +56,10 @@ struct Prob {
     const void* grid;   // ns x nz, row-major: grid[i*nz + j] = K(sbins[i], zbins[j])
     int64_t ns, nz;
     double alpha;
+    // Accumulate the d/dvals histograms in double instead of T. The reference sums in T
+    // (src/grad.jl:32-87), so the default mirrors it; the double mode removes the summation
+    // noise of very large point sets from comparisons whose subject is the per-point arithmetic.
+    int acc64;
 };
 
 template <typename T> inline T eps_of();
@@ -273,19 +277,19 @@ inline void factor_point(Scratch<T>& s, const Prob& p, int64_t m, T scale, const
 
 // Scatter a lower-triangle cotangent through the lookup weights into dv (dv[0] gets every
 // diagonal, one add per row, as src/grad.jl:43-56). `r` without @fastmath there.
-template <typename T>
-inline void scatter_abar(T* dv, const Scratch<T>& s, T scale, const T* bins, int64_t nb, int64_t D) {
+template <typename T, typename A>
+inline void scatter_abar(A* dv, const Scratch<T>& s, T scale, const T* bins, int64_t nb, int64_t D) {
     const int64_t n = s.n;
     for (int64_t a = 0; a < n; ++a) {
-        dv[0] += s.Abar[a * n + a];
+        dv[0] += (A)s.Abar[a * n + a];
         for (int64_t b = 0; b < a; ++b) {
             int64_t sq = sqdist(s.jc.data() + a * D, s.jc.data() + b * D, D);
             T r = std::sqrt(T(sq)) * scale;
             int64_t lo; T wlo, whi;
             cov_lookup_weights(r, bins, nb, lo, wlo, whi);
             T g = s.Abar[a * n + b];
-            dv[lo] += g * wlo;
-            dv[lo + 1] += g * whi;
+            dv[lo] += (A)(g * wlo);
+            dv[lo + 1] += (A)(g * whi);
         }
     }
 }
@@ -441,10 +445,31 @@ bool potrf_lower(const T* Kd, int64_t n, T* L) {
         if (!(s > T(0))) return false;
         T d = std::sqrt(s);
         L[j * n + j] = d;
-        for (int64_t i = j + 1; i < n; ++i) {
-            T t = L[i * n + j];
-            for (int64_t p = 0; p < j; ++p) t = std::fma(-L[i * n + p], L[j * n + p], t);
-            L[i * n + j] = t / d;
+        // Rows are independent within a column; each keeps its own fma chain in p order. Four
+        // rows per iteration only interleave four independent chains.
+        const int64_t r0 = j + 1, nr = n - r0, nq = (nr + 3) / 4;
+#pragma omp parallel for schedule(static) if (nr > 256)
+        for (int64_t q = 0; q < nq; ++q) {
+            const int64_t i = r0 + 4 * q;
+            const T* lj = L + j * n;
+            if (i + 3 < n) {
+                T* a = L + i * n; T* b = a + n; T* c = b + n; T* e = c + n;
+                T t0 = a[j], t1 = b[j], t2 = c[j], t3 = e[j];
+                for (int64_t p = 0; p < j; ++p) {
+                    const T lp = lj[p];
+                    t0 = std::fma(-a[p], lp, t0);
+                    t1 = std::fma(-b[p], lp, t1);
+                    t2 = std::fma(-c[p], lp, t2);
+                    t3 = std::fma(-e[p], lp, t3);
+                }
+                a[j] = t0 / d; b[j] = t1 / d; c[j] = t2 / d; e[j] = t3 / d;
+            } else {
+                for (int64_t ii = i; ii < n; ++ii) {
+                    T t = L[ii * n + j];
+                    for (int64_t p = 0; p < j; ++p) t = std::fma(-L[ii * n + p], lj[p], t);
+                    L[ii * n + j] = t / d;
+                }
+            }
         }
     }
     return true;
@@ -614,7 +639,8 @@ void refine_logdet_grad_vals(const Prob& p, T* dvals, double* logdet) {
     const T* bins = (const T*)p.bins; const T* vals = (const T*)p.vals; const T scale = T(p.scale);
     const int64_t M = p.N - p.n0, K = p.K, nb = p.nbins;
     int nch = (int)std::max<int64_t>(1, std::min<int64_t>(p.nthreads, M));
-    std::vector<std::vector<T>> dvs(nch, std::vector<T>(nb, T(0)));
+    std::vector<std::vector<T>> dvs(nch, std::vector<T>(p.acc64 ? 0 : nb, T(0)));
+    std::vector<std::vector<double>> dvs64(nch, std::vector<double>(p.acc64 ? nb : 0, 0.0));
     std::vector<T> lds(nch, T(0));
     if (M > 0) {
         int64_t chunk = (M + nch - 1) / nch;
@@ -628,7 +654,8 @@ void refine_logdet_grad_vals(const Prob& p, T* dvals, double* logdet) {
                 zero_lbar(s.Lbar.data(), s.n);
                 s.Lbar[K * s.n + K] = T(1) / s.A[K * s.n + K];  // linalg.jl:140-146, seed 1
                 chol_pullback_impl<T, false>(s.Abar.data(), s.Lbar.data(), s.A.data(), s.n);
-                scatter_abar(dvs[c].data(), s, scale, bins, nb, p.D);
+                if (p.acc64) scatter_abar(dvs64[c].data(), s, scale, bins, nb, p.D);
+                else scatter_abar(dvs[c].data(), s, scale, bins, nb, p.D);
                 lds[c] += ldt;
             }
         }
@@ -637,8 +664,15 @@ void refine_logdet_grad_vals(const Prob& p, T* dvals, double* logdet) {
     for (int64_t i = 0; i < nb; ++i) dvals[i] = T(0);
     for (int c = 0; c < nch; ++c) {
         ld += lds[c];
-        for (int64_t i = 0; i < nb; ++i) dvals[i] += dvs[c][i];
+        if (!p.acc64)
+            for (int64_t i = 0; i < nb; ++i) dvals[i] += dvs[c][i];
     }
+    if (p.acc64)
+        for (int64_t i = 0; i < nb; ++i) {
+            double t = 0.0;
+            for (int c = 0; c < nch; ++c) t += dvs64[c][i];
+            dvals[i] = (T)t;
+        }
     if (logdet) *logdet = (double)ld;
 }
 
@@ -664,7 +698,8 @@ void refine_inv_loss_grad_vals(const Prob& p, const T* values, T* dvals, double*
     const T* bins = (const T*)p.bins; const T* vals = (const T*)p.vals; const T scale = T(p.scale);
     const int64_t M = p.N - p.n0, K = p.K, nb = p.nbins, n0 = p.n0;
     int nch = (int)std::max<int64_t>(1, std::min<int64_t>(p.nthreads, M));
-    std::vector<std::vector<T>> dvs(nch, std::vector<T>(nb, T(0)));
+    std::vector<std::vector<T>> dvs(nch, std::vector<T>(p.acc64 ? 0 : nb, T(0)));
+    std::vector<std::vector<double>> dvs64(nch, std::vector<double>(p.acc64 ? nb : 0, 0.0));
     std::vector<T> ls(nch, T(0));
     if (M > 0) {
         int64_t chunk = (M + nch - 1) / nch;
@@ -693,7 +728,8 @@ void refine_inv_loss_grad_vals(const Prob& p, const T* values, T* dvals, double*
                     for (int64_t i = 0; i <= j; ++i) s.Lbar[j * n + i] -= s.zbar[i] * s.mv[j];
                 }
                 chol_pullback_impl<T, false>(s.Abar.data(), s.Lbar.data(), s.A.data(), n);
-                scatter_abar(dvs[c].data(), s, scale, bins, nb, p.D);
+                if (p.acc64) scatter_abar(dvs64[c].data(), s, scale, bins, nb, p.D);
+                else scatter_abar(dvs[c].data(), s, scale, bins, nb, p.D);
                 ls[c] += xi_m * xi_m / T(2);
             }
         }
@@ -702,8 +738,15 @@ void refine_inv_loss_grad_vals(const Prob& p, const T* values, T* dvals, double*
     for (int64_t i = 0; i < nb; ++i) dvals[i] = T(0);
     for (int c = 0; c < nch; ++c) {
         l += ls[c];
-        for (int64_t i = 0; i < nb; ++i) dvals[i] += dvs[c][i];
+        if (!p.acc64)
+            for (int64_t i = 0; i < nb; ++i) dvals[i] += dvs[c][i];
     }
+    if (p.acc64)
+        for (int64_t i = 0; i < nb; ++i) {
+            double t = 0.0;
+            for (int c = 0; c < nch; ++c) t += dvs64[c][i];
+            dvals[i] = (T)t;
+        }
     if (loss) *loss = (double)l;
 }
 
@@ -780,6 +823,11 @@ int generate_grad_vals(const Prob& p, const T* xi, const T* vbar, T* dvals) {
         }
     for (int64_t i = 0; i < N; ++i) vb[i] = p.indices ? vbar[p.indices[i]] : vbar[i];
     for (int64_t i = 0; i < nb; ++i) dvals[i] = T(0);
+    std::vector<double> dv64(p.acc64 ? nb : 0, 0.0);
+    auto add = [&](int64_t bin, T g) {
+        if (p.acc64) dv64[bin] += (double)g;
+        else dvals[bin] += g;
+    };
     Scratch<T> s(K, D);
     const int64_t n = s.n;
     const T pivfloor_c = T(1.5) * std::sqrt(eps_of<T>());
@@ -809,7 +857,8 @@ int generate_grad_vals(const Prob& p, const T* xi, const T* vbar, T* dvals) {
                 for (int64_t i = 0; i <= j; ++i) s.Lbar[j * n + i] -= s.zbar[i] * s.mv[j];
             }
             chol_pullback_impl<T, false>(s.Abar.data(), s.Lbar.data(), s.A.data(), n);
-            scatter_abar(dvals, s, scale, bins, nb, D);
+            if (p.acc64) scatter_abar(dv64.data(), s, scale, bins, nb, D);
+            else scatter_abar(dvals, s, scale, bins, nb, D);
             for (int64_t j = 0; j < K; ++j) {
                 int64_t nbj = p.neighbors[m * K + j];
                 if (nbj >= 0) vb[nbj] += mv[m * K + j] * vbp;
@@ -821,17 +870,19 @@ int generate_grad_vals(const Prob& p, const T* xi, const T* vbar, T* dvals) {
         for (int64_t i = j; i < n0; ++i) Lbar_d[i * n0 + j] = vb[i] * xih[j];
     chol_pullback_impl<T, true>(Kbar_d.data(), Lbar_d.data(), L.data(), n0);
     for (int64_t j = 0; j < n0; ++j) {
-        dvals[0] += Kbar_d[j * n0 + j];
+        add(0, Kbar_d[j * n0 + j]);
         for (int64_t i = j + 1; i < n0; ++i) {
             int64_t sq = sqdist(p.coords + i * D, p.coords + j * D, D);
             T r = std::sqrt(T(sq)) * scale;
             int64_t lo; T wlo, whi;
             cov_lookup_weights(r, bins, nb, lo, wlo, whi);
             T g = Kbar_d[i * n0 + j];
-            dvals[lo] += g * wlo;
-            dvals[lo + 1] += g * whi;
+            add(lo, g * wlo);
+            add(lo + 1, g * whi);
         }
     }
+    if (p.acc64)
+        for (int64_t i = 0; i < nb; ++i) dvals[i] = (T)dv64[i];
     return 0;
 }
 

@@ -43,6 +43,7 @@ class _Prob(C.Structure):
         ("ns", C.c_int64),
         ("nz", C.c_int64),
         ("alpha", C.c_double),
+        ("acc64", C.c_int),
     ]
 
 
@@ -73,9 +74,10 @@ class Problem:
     """A refinement problem held in numpy arrays, in the oracle's (and the HIP ABI's) layout."""
 
     def __init__(self, coords, neighbors, offsets, n0, scale, bins, vals, indices=None,
-                 dtype=np.float64, nthreads=None, aniso=None):
+                 dtype=np.float64, nthreads=None, aniso=None, acc64=False):
         """aniso: optional (spatial_bins, z_bins, grid (ns, nz), alpha) — the anisotropic
-        covariance, which then replaces (bins, vals) (src/aniso.jl)."""
+        covariance, which then replaces (bins, vals) (src/aniso.jl). acc64: sum the d/dvals
+        histograms in double (the reference sums in the element type)."""
         self.dtype = np.dtype(dtype)
         self.coords = np.ascontiguousarray(coords, dtype=np.uint32)
         self.neighbors = np.ascontiguousarray(neighbors, dtype=np.int64)
@@ -91,6 +93,7 @@ class Problem:
         assert self.neighbors.shape[0] == self.M
         self.nthreads = int(nthreads or os.cpu_count() or 1)
         self.aniso = aniso
+        self.acc64 = bool(acc64)
         if aniso is not None:
             sb, zb, grid, alpha = aniso
             self._sb = np.ascontiguousarray(sb, dtype=self.dtype)
@@ -104,17 +107,17 @@ class Problem:
         self._s = _Prob(_ptr(self.coords), _ptr(self.neighbors), _ptr(self.offsets),
                         _ptr(self.indices), len(self.offsets), self.n0, self.K, self.N, self.D,
                         len(self.bins), self.scale, _ptr(self.bins), _ptr(self.vals),
-                        self.nthreads, *an)
+                        self.nthreads, *an, int(self.acc64))
 
     # the struct keeps raw pointers: keep arrays alive via self
     def with_vals(self, vals):
         return Problem(self.coords, self.neighbors, self.offsets, self.n0, self.scale, self.bins,
-                       vals, self.indices, self.dtype, self.nthreads, self.aniso)
+                       vals, self.indices, self.dtype, self.nthreads, self.aniso, self.acc64)
 
     def with_dtype(self, dtype):
         return Problem(self.coords, self.neighbors, self.offsets, self.n0, self.scale,
                        self.bins.astype(dtype), self.vals.astype(dtype), self.indices, dtype,
-                       self.nthreads, self.aniso)
+                       self.nthreads, self.aniso, self.acc64)
 
     @property
     def _sfx(self):
