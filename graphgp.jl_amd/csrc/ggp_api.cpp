@@ -322,7 +322,7 @@ int dense_retry(ggp_graph* h) {
     while (e <= T(1e-2)) {
         launch_fill<int>(h->info, 0, 1, h->s_main);
         dense_assemble<T>(h->g, tb, tp<T>(h->A), e * dmean, h->s_main);
-        dense_potrf<T>(tp<T>(h->A), n, h->info, h->dsync, std::max(1, h->ncu / 2), h->s_main);
+        dense_potrf<T>(tp<T>(h->A), n, h->info, h->dsync, std::max(1, h->ncu / 4), h->s_main);
         HC(hipMemcpyAsync(h->hinfo, h->info, sizeof(int), hipMemcpyDeviceToHost, h->s_main));
         HC(hipStreamSynchronize(h->s_main));
         if (*h->hinfo == 0) return 0;
@@ -339,7 +339,7 @@ void dense_factor_async(ggp_graph* h, hipStream_t st) {
     tstart(h, TM_DENSE, st);
     launch_fill<int>(h->info, 0, 1, st);
     dense_assemble<T>(h->g, table<T>(h), tp<T>(h->A), T(0), st);
-    dense_potrf<T>(tp<T>(h->A), (int)h->g.n0, h->info, h->dsync, std::max(1, h->ncu / 2), st);
+    dense_potrf<T>(tp<T>(h->A), (int)h->g.n0, h->info, h->dsync, std::max(1, h->ncu / 4), st);
     tstop(h, TM_DENSE, st);
 }
 
