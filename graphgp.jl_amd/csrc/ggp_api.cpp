@@ -284,6 +284,7 @@ int join(ggp_graph* h) {
 // Drain the main stream, release the user stream, and fetch info + scalars.
 int finish(ggp_graph* h, hipStream_t user) {
     HC(hipMemcpyAsync(h->hinfo, h->info, sizeof(int), hipMemcpyDeviceToHost, h->s_main));
+    HC(hipMemcpyAsync(h->hinfo + 1, h->g.sweep_err, sizeof(int), hipMemcpyDeviceToHost, h->s_main));
     HC(hipMemcpyAsync(h->hscal, h->dscal, 8 * sizeof(double), hipMemcpyDeviceToHost, h->s_main));
     HC(hipGetLastError());
     tstop(h, TM_OP, h->s_main);
@@ -291,6 +292,11 @@ int finish(ggp_graph* h, hipStream_t user) {
     HC(hipStreamWaitEvent(user, h->ev_user, 0));
     HC(hipStreamSynchronize(h->s_main));
     tcollect(h);
+    if (h->hinfo[1] & 4) {
+        h->hinfo[1] = 0;
+        (void)hipMemset(h->g.sweep_err, 0, sizeof(int));
+        return fail(GGP_ERR_HIP, "level sweep: a wait for an input value timed out");
+    }
     return 0;
 }
 
@@ -375,32 +381,24 @@ int check_ready(ggp_graph* h) {
     return 0;
 }
 
-// Forward sweep over all depth levels (src/api.jl:126-137); xi indexed as xi[xi_off + m].
+// Forward sweep over all depth levels (src/api.jl:126-137), one launch; xi indexed as
+// xi[xi_off + m].
 template <typename T>
 void sweep_forward(ggp_graph* h, T* v, const T* xi, int64_t xi_off, hipStream_t st) {
     const Graph& g = h->g;
     tstart(h, TM_SWEEP_FWD, st);
-    for (size_t b = 1; b < g.offsets.size(); ++b) {
-        const int64_t len = g.offsets[b] - g.offsets[b - 1];
-        if (len <= 0) continue;
-        launch_sweep_fwd<T>(g, v, xi, xi_off, tp<T>(h->mv), tp<T>(h->sd), g.offsets[b - 1] - g.n0,
-                            len, table<T>(h).aniso.grid != nullptr, st);
-    }
+    launch_sweep_fwd<T>(g, v, xi, xi_off, tp<T>(h->mv), tp<T>(h->sd),
+                        table<T>(h).aniso.grid != nullptr, st);
     tstop(h, TM_SWEEP_FWD, st);
 }
 
-// Reverse sweep, latest level first, then the dense level (src/grad.jl:433-445, 483-489).
+// Reverse sweep, latest level first, then the dense level (src/grad.jl:433-445, 483-489), one
+// launch.
 template <typename T>
 void sweep_reverse(ggp_graph* h, T* vb, const T* vbar, T* xg, hipStream_t st) {
     const Graph& g = h->g;
     tstart(h, TM_SWEEP_REV, st);
-    for (size_t b = g.offsets.size() - 1; b >= 1; --b) {
-        if (g.offsets[b] > g.offsets[b - 1])
-            launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), g.offsets[b - 1],
-                                g.offsets[b], g.rev_group[b], st);
-    }
-    if (g.n0 > 0)
-        launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), 0, g.n0, g.rev_group[0], st);
+    launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), st);
     tstop(h, TM_SWEEP_REV, st);
 }
 
@@ -743,16 +741,20 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
                 rev[(size_t)pos[(size_t)q]++] = (uint32_t)(m * k + j);
             }
     }
-    // lanes per point of the reverse sweep: the power of two covering the level's largest fan-in
-    g.rev_group.assign((size_t)n_off, 1);
-    for (int64_t b = 0; b < n_off; ++b) {
+    // Chunk lists of the one-launch sweeps (within one level each, topological order).
+    std::vector<int4> fch, rch;
+    for (int64_t b = 1; b < n_off; ++b)
+        for (int64_t s0 = offs[b - 1]; s0 < offs[b]; s0 += kBlock)
+            fch.push_back(make_int4((int)(s0 - n0), (int)std::min<int64_t>(kBlock, offs[b] - s0), 0, 0));
+    for (int64_t b = n_off - 1; b >= 0; --b) {
         const int64_t lo = b == 0 ? 0 : offs[b - 1], hi = b == 0 ? n0 : offs[b];
-        int64_t mx = 0;
-        for (int64_t q = lo; q < hi; ++q) mx = std::max(mx, rptr[(size_t)q + 1] - rptr[(size_t)q]);
-        int G = 1;
-        while (G < mx && G < 64) G <<= 1;
-        g.rev_group[(size_t)b] = G;
+        for (int64_t s0 = lo; s0 < hi; s0 += kBlock)
+            rch.push_back(make_int4((int)s0, (int)std::min<int64_t>(kBlock, hi - s0), 0, 0));
     }
+    g.n_fwd_chunks = (int)fch.size();
+    g.n_rev_chunks = (int)rch.size();
+    g.sweep_wgs = h->ncu;
+    if (const char* e = std::getenv("GGP_SWEEP_WGS_PER_CU")) g.sweep_wgs = h->ncu * std::max(1, atoi(e));
     std::vector<int32_t> idx32;
     if (indices) {
         idx32.resize((size_t)N);
@@ -777,6 +779,10 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     rc |= dmalloc(h, (void**)&h->dscal, 8 * 8);
     rc |= dmalloc(h, (void**)&h->info, 16);
     rc |= dmalloc(h, (void**)&h->dsync, (size_t)dense_sync_ints((int)n0) * sizeof(int));
+    rc |= dmalloc(h, (void**)&g.fwd_chunks, std::max<size_t>(fch.size(), 1) * sizeof(int4));
+    rc |= dmalloc(h, (void**)&g.rev_chunks, std::max<size_t>(rch.size(), 1) * sizeof(int4));
+    rc |= dmalloc(h, (void**)&g.sweep_ticket, 16);
+    rc |= dmalloc(h, (void**)&g.sweep_err, 16);
     if (rc) return bail(GGP_ERR_HIP);
     if (hipHostMalloc((void**)&h->hscal, 8 * 8) != hipSuccess ||
         hipHostMalloc((void**)&h->hinfo, 16) != hipSuccess)
@@ -785,7 +791,10 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
         hipMemcpy(g.nbr, nsoa.data(), nsoa.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(g.rev_ptr, rptr.data(), rptr.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(g.rev, rev.data(), rev.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        (indices && hipMemcpy(g.idx, idx32.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess))
+        (indices && hipMemcpy(g.idx, idx32.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess) ||
+        (!fch.empty() && hipMemcpy(g.fwd_chunks, fch.data(), fch.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess) ||
+        (!rch.empty() && hipMemcpy(g.rev_chunks, rch.data(), rch.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess) ||
+        hipMemset(g.sweep_err, 0, 16) != hipSuccess)
         return bail(fail(GGP_ERR_HIP, "hipMemcpy of the graph failed"));
     if (hipStreamCreateWithFlags(&h->s_main, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&h->s_side, hipStreamNonBlocking) != hipSuccess ||

@@ -25,7 +25,15 @@ struct Graph {
     int64_t* rev_ptr = nullptr;    // N+1: consumers of point q are rev[rev_ptr[q] .. rev_ptr[q+1])
     uint32_t* rev = nullptr;       // m*K + j of each consumer, by decreasing consumer position
     std::vector<int64_t> offsets;  // host copy, offsets[0] = n0
-    std::vector<int> rev_group;    // lanes per point of the reverse sweep, per level (0 = dense)
+    // Work lists of the one-launch sweeps: chunks of one level each, in topological order.
+    // fwd: {first refined index m, points, 0, 0}; rev: {first position q, points, 0, 0}, latest
+    // level first, the dense block last.
+    int4* fwd_chunks = nullptr;
+    int4* rev_chunks = nullptr;
+    int n_fwd_chunks = 0, n_rev_chunks = 0;
+    int* sweep_ticket = nullptr;   // 1 int, zeroed before each sweep
+    int* sweep_err = nullptr;      // bit 2: a wait ran past its bound
+    int sweep_wgs = 1024;          // workgroups of a sweep launch
 };
 
 // Device-resident covariance table prepared for O(1) segment lookup.
@@ -54,9 +62,9 @@ struct PointK {
                          const T* vb, double* hist_partial, double* scalar_partial,
                          unsigned nblk, hipStream_t st);
     static void sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                          const T* sd, int64_t m_lo, int64_t len, bool two_pass, hipStream_t st);
+                          const T* sd, bool two_pass, hipStream_t st);
     static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                          int64_t q_lo, int64_t q_hi, int G, hipStream_t st);
+                          hipStream_t st);
 };
 // The same launchers for any k <= 31 (wavefront-per-point kernels, ggp_wide.h).
 template <typename T>
@@ -68,9 +76,9 @@ struct WideK {
                          const T* vb, double* hist_partial, double* scalar_partial,
                          unsigned nblk, hipStream_t st);
     static void sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                          const T* sd, int64_t m_lo, int64_t len, bool two_pass, hipStream_t st);
+                          const T* sd, bool two_pass, hipStream_t st);
     static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                          int64_t q_lo, int64_t q_hi, int G, hipStream_t st);
+                          hipStream_t st);
 };
 extern template struct WideK<float>;
 extern template struct WideK<double>;
@@ -110,14 +118,19 @@ template <typename T>
 void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, const T* xi,
                      const T* vb, double* hist_partial, double* scalar_partial, unsigned nblk,
                      hipStream_t st);
+// Whole sweeps, one launch each: the forward apply over every level (v[n0:end] is written) and
+// the reverse gather (vb and xg of every position in a level or the dense block).
 template <typename T>
 void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                      const T* sd, int64_t m_lo, int64_t len, bool two_pass, hipStream_t st);
+                      const T* sd, bool two_pass, hipStream_t st);
 template <typename T>
 void launch_sumsq_half(const T* x, int64_t n, double* out, hipStream_t st);
 template <typename T>
 void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                      int64_t q_lo, int64_t q_hi, int G, hipStream_t st);
+                      hipStream_t st);
+// p[0:n] = the pending marker of the sweeps (a NaN no arithmetic produces).
+template <typename T>
+void launch_fill_pending(T* p, int64_t n, hipStream_t st);
 template <typename T>
 void launch_reduce_hist(T* d_out, const double* partial, int nw, int nb, const double* extra,
                         hipStream_t st);

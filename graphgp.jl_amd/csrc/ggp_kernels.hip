@@ -112,22 +112,14 @@ void WideK<T>::pullback(const Graph& g, const Table<T>& tb, int mode, const T* v
 
 template <typename T>
 void WideK<T>::sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                         const T* sd, int64_t m_lo, int64_t len, bool two_pass,
-                         hipStream_t st) {
-    if (two_pass)
-        hipLaunchKernelGGL((k_sweep_fwd<T, 0, true>), dim3(grid_for_pt(len)), dim3(kBlock), 0, st,
-                           v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len, (int)g.K);
-    else
-        hipLaunchKernelGGL((k_sweep_fwd<T, 0, false>), dim3(grid_for_pt(len)), dim3(kBlock), 0,
-                           st, v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len, (int)g.K);
+                         const T* sd, bool two_pass, hipStream_t st) {
+    PointK<T, 0>::sweep_fwd(g, v, xi, xi_off, mv, sd, two_pass, st);
 }
 
 template <typename T>
 void WideK<T>::sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                         int64_t q_lo, int64_t q_hi, int G, hipStream_t st) {
-    hipLaunchKernelGGL((k_sweep_rev<T, 0>), dim3(grid_for_pt((q_hi - q_lo) * G)), dim3(kBlock), 0,
-                       st, vb, vbar, xg, mv, sd, g.rev_ptr, g.rev, g.M, g.n0, q_lo, q_hi, G,
-                       (int)g.K);
+                         hipStream_t st) {
+    PointK<T, 0>::sweep_rev(g, vb, vbar, xg, mv, sd, st);
 }
 
 template struct WideK<float>;
@@ -173,18 +165,37 @@ void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, c
 
 template <typename T>
 void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                      const T* sd, int64_t m_lo, int64_t len, bool two_pass, hipStream_t st) {
-#define CALLS(KK) Launch<T, KK>::sweep_fwd(g, v, xi, xi_off, mv, sd, m_lo, len, two_pass, st)
+                      const T* sd, bool two_pass, hipStream_t st) {
+    if (g.n_fwd_chunks == 0) return;
+    launch_fill<int>(g.sweep_ticket, 0, 1, st);
+    launch_fill_pending<T>(v + g.n0, g.offsets.back() - g.n0, st);
+#define CALLS(KK) Launch<T, KK>::sweep_fwd(g, v, xi, xi_off, mv, sd, two_pass, st)
     GGP_FOR_K(CALLS);
 #undef CALLS
 }
 
 template <typename T>
 void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                      int64_t q_lo, int64_t q_hi, int G, hipStream_t st) {
-#define CALLR(KK) Launch<T, KK>::sweep_rev(g, vb, vbar, xg, mv, sd, q_lo, q_hi, G, st)
+                      hipStream_t st) {
+    if (g.n_rev_chunks == 0) return;
+    launch_fill<int>(g.sweep_ticket, 0, 1, st);
+    launch_fill_pending<T>(vb + g.n0, g.offsets.back() - g.n0, st);
+#define CALLR(KK) Launch<T, KK>::sweep_rev(g, vb, vbar, xg, mv, sd, st)
     GGP_FOR_K(CALLR);
 #undef CALLR
+}
+
+template <typename U>
+__global__ void k_fill_bits(U* __restrict__ p, U v, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+template <typename T>
+void launch_fill_pending(T* p, int64_t n, hipStream_t st) {
+    using U = typename num<T>::bits_t;
+    if (n > 0)
+        hipLaunchKernelGGL((k_fill_bits<U>), dim3(grid_for(n)), dim3(kBlock), 0, st,
+                           reinterpret_cast<U*>(p), (U)Pending<T>::bits, n);
 }
 
 template <typename T>
@@ -222,9 +233,10 @@ void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st) {
     template void launch_pullback<T>(const Graph&, const Table<T>&, int, const T*, const T*,   \
                                      const T*, double*, double*, unsigned, hipStream_t);       \
     template void launch_sweep_fwd<T>(const Graph&, T*, const T*, int64_t, const T*, const T*, \
-                                      int64_t, int64_t, bool, hipStream_t);                    \
+                                      bool, hipStream_t);                                      \
     template void launch_sweep_rev<T>(const Graph&, T*, const T*, T*, const T*, const T*,      \
-                                      int64_t, int64_t, int, hipStream_t);                     \
+                                      hipStream_t);                                            \
+    template void launch_fill_pending<T>(T*, int64_t, hipStream_t);                            \
     template void launch_reduce_hist<T>(T*, const double*, int, int, const double*,            \
                                         hipStream_t);                                          \
     template void launch_gather<T>(T*, const T*, const int32_t*, int64_t, hipStream_t);        \

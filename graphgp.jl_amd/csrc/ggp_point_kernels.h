@@ -106,89 +106,167 @@ k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, i
     }
 }
 
-// ---- level sweeps ---------------------------------------------------------------------------
-// Forward apply of one depth level (src/kernels.jl:113-118): std*xi first, then + mv_j*v_j in
-// neighbour order, each product rounded before the add (that code is not under @fastmath).
-// TWO_PASS: the anisotropic apply order (src/kernels.jl:89-92): sum mv_j*v_j first, then
-// + std*xi.
-// K = 0: k is the run-time Krt (the wavefront-per-point path); otherwise Krt == K.
+// ---- level sweeps: one persistent launch per sweep ----------------------------------------
+// Every value a sweep produces starts as a pending marker (a NaN no arithmetic produces) and is
+// published once, with an agent-scope store. A reader takes its inputs with plain loads and
+// polls with agent-scope loads only those it still sees pending: a published value never
+// changes, so a plain load returns either the marker or the final value.
+//
+// Workgroups take chunks from an atomic ticket counter; the chunks lie inside one level each
+// and are listed in topological order (a point's inputs sit in strictly earlier chunks), so a
+// chunk only waits for chunks already taken by running workgroups, whatever the residency,
+// and no wavefront ever waits for a lane of its own. Every wait is bounded: past
+// kSweepSpinLimit polls it sets bit 2 of *err and goes on, so every workgroup exits; the host
+// reports that as an error. The arithmetic per point is the per-level kernels', unchanged.
+template <typename T> struct Pending;
+template <> struct Pending<float> { static constexpr uint32_t bits = 0x7fc0feedu; };
+template <> struct Pending<double> { static constexpr uint64_t bits = 0x7ff800000000feedull; };
+constexpr int kSweepSpinLimit = 1 << 20;
+
+__device__ inline float from_bits(uint32_t b) { return __uint_as_float(b); }
+__device__ inline double from_bits(uint64_t b) { return __longlong_as_double((long long)b); }
+
+// Values at p[idx[u]] for the live entries u < B (live[u] false: 0). All reads are issued
+// together; the ones still pending are polled together, one back-off sleep per round.
+template <typename T, int B>
+__device__ inline void sweep_read_all(T (&out)[B], const T* p, const int64_t (&idx)[B],
+                                      const bool (&live)[B], int* err) {
+    using U = typename num<T>::bits_t;
+    const U* pu = reinterpret_cast<const U*>(p);
+    U b[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) b[u] = live[u] ? pu[idx[u]] : U(0);
+    for (int spins = 0;; ++spins) {
+        bool pending = false;
+#pragma unroll
+        for (int u = 0; u < B; ++u) pending = pending || b[u] == Pending<T>::bits;
+        if (!pending) break;
+        if (spins > kSweepSpinLimit) {
+            atomicOr(err, 4);
+            break;
+        }
+        if (spins < 4) __builtin_amdgcn_s_sleep(1);
+        else if (spins < 16) __builtin_amdgcn_s_sleep(4);
+        else __builtin_amdgcn_s_sleep(16);
+#pragma unroll
+        for (int u = 0; u < B; ++u)
+            if (b[u] == Pending<T>::bits)
+                b[u] = __hip_atomic_load(pu + idx[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) out[u] = live[u] ? from_bits(b[u]) : T(0);
+}
+
+template <typename T>
+__device__ inline void sweep_publish(T* p, T x) {
+    using U = typename num<T>::bits_t;
+    __hip_atomic_store(reinterpret_cast<U*>(p), num<T>::bits(x), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Next chunk for the workgroup; the value is made wave-uniform for the compiler (readfirstlane)
+// so the loop test is a uniform branch and the loop keeps its shape.
+__device__ inline int sweep_next(int* ticket, int* s_c) {
+    __syncthreads();
+    if (threadIdx.x == 0) *s_c = atomicAdd(ticket, 1);
+    __syncthreads();
+    return __builtin_amdgcn_readfirstlane(*s_c);
+}
+
+// Forward apply (src/kernels.jl:113-118): std*xi first, then + mv_j*v_j in neighbour order, each
+// product rounded before the add (that code is not under @fastmath). TWO_PASS: the anisotropic
+// order (src/kernels.jl:89-92): sum mv_j*v_j first, then + std*xi. K = 0: k is the run-time Krt.
 template <typename T, int K, bool TWO_PASS>
 __global__ void __launch_bounds__(kBlock)
 k_sweep_fwd(T* __restrict__ v, const T* __restrict__ xi, int64_t xi_off,
             const T* __restrict__ mv, const T* __restrict__ sd, const int32_t* __restrict__ nbr,
-            int64_t M, int64_t n0, int64_t m_lo, int64_t len, int Krt) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= len) return;
-    const int64_t m = m_lo + t;
-    if constexpr (K == 0) {
-        T acc = TWO_PASS ? T(0) : sd[m] * xi[xi_off + m];
-        for (int j = 0; j < Krt; ++j)
-            acc = acc + mv[(int64_t)j * M + m] * v[nbr[(int64_t)j * M + m]];
-        v[n0 + m] = TWO_PASS ? acc + sd[m] * xi[xi_off + m] : acc;
-        return;
-    }
+            int64_t M, int64_t n0, int Krt, const int4* __restrict__ chunks, int nchunks,
+            int* __restrict__ ticket, int* __restrict__ err) {
+    __shared__ int s_c;
     constexpr int KA = K > 0 ? K : 1;
-    int32_t nb[KA];
-    T w[KA];
+    for (int c = sweep_next(ticket, &s_c); c < nchunks; c = sweep_next(ticket, &s_c)) {
+        const int4 ch = chunks[c];
+        if ((int)threadIdx.x >= ch.y) continue;
+        const int64_t m = ch.x + threadIdx.x;
+        const T s_xi = sd[m] * xi[xi_off + m];
+        T acc = TWO_PASS ? T(0) : s_xi;
+        if constexpr (K == 0) {
+            constexpr int B = 8;
+            for (int j0 = 0; j0 < Krt; j0 += B) {
+                int64_t q[B];
+                bool live[B];
+                T w[B], x[B];
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-        nb[j] = nbr[(int64_t)j * M + m];
-        w[j] = mv[(int64_t)j * M + m];
-    }
-    if (TWO_PASS) {
-        T acc = T(0);
+                for (int u = 0; u < B; ++u) {
+                    live[u] = j0 + u < Krt;
+                    q[u] = live[u] ? nbr[(int64_t)(j0 + u) * M + m] : 0;
+                    w[u] = live[u] ? mv[(int64_t)(j0 + u) * M + m] : T(0);
+                }
+                sweep_read_all<T, B>(x, v, q, live, err);
 #pragma unroll
-        for (int j = 0; j < K; ++j) acc = acc + w[j] * v[nb[j]];
-        v[n0 + m] = acc + sd[m] * xi[xi_off + m];
-    } else {
-        T acc = sd[m] * xi[xi_off + m];
+                for (int u = 0; u < B; ++u)
+                    if (live[u]) acc = acc + w[u] * x[u];
+            }
+        } else {
+            int64_t q[KA];
+            bool live[KA];
+            T w[KA], x[KA];
 #pragma unroll
-        for (int j = 0; j < K; ++j) acc = acc + w[j] * v[nb[j]];
-        v[n0 + m] = acc;
+            for (int j = 0; j < K; ++j) {
+                q[j] = nbr[(int64_t)j * M + m];
+                w[j] = mv[(int64_t)j * M + m];
+                live[j] = true;
+            }
+            sweep_read_all<T, KA>(x, v, q, live, err);
+#pragma unroll
+            for (int j = 0; j < K; ++j) acc = acc + w[j] * x[j];
+        }
+        if (TWO_PASS) acc = acc + s_xi;
+        sweep_publish(v + n0 + m, acc);
     }
 }
 
-// Reverse sweep of one depth level, positions [q_lo, q_hi): vb[q] = vbar[q] + sum over the
-// consumers (p, j) of q of mv_j(p)*vb[p], the consumers listed by decreasing p — exactly the
-// order in which the reference's serial host sweep (src/grad.jl:433-445) adds them — and
-// xg[q] = std_q*vb[q] for refined q. Every consumer lies in a later level, so vb[p] is final.
-//
-// A group of G lanes (G a power of two <= 64, sized to the level's largest fan-in) serves one
-// point: each lane loads one consumer's product mv*vb per round, so the dependent memory round
-// trips per point drop from the fan-in to fan-in/G; the products are then added one by one in
-// list order (shuffled from their lanes), which keeps every rounding of the serial sum.
+// Reverse gather (the transpose of the forward apply): vb[q] = vbar[q] + sum over the consumers
+// (p, j) of q of mv_j(p)*vb[p], the consumers listed by decreasing p — exactly the order in
+// which the reference's serial host sweep (src/grad.jl:433-445) adds them — and
+// xg[q] = std_q*vb[q] for refined q. One lane per point; the consumers are fetched kRevBatch at a
+// time (independent loads in flight together) and their products added one by one in list
+// order, which keeps every rounding of the serial sum.
+constexpr int kRevBatch = 8;
 template <typename T, int K>
 __global__ void __launch_bounds__(kBlock)
 k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
             const T* __restrict__ mv, const T* __restrict__ sd,
-            const int64_t* __restrict__ rev_ptr, const uint32_t* __restrict__ rev,
-            int64_t M, int64_t n0, int64_t q_lo, int64_t q_hi, int G, int Krt) {
+            const int64_t* __restrict__ rev_ptr, const uint32_t* __restrict__ rev, int64_t M,
+            int64_t n0, int Krt, const int4* __restrict__ chunks, int nchunks,
+            int* __restrict__ ticket, int* __restrict__ err) {
+    __shared__ int s_c;
     const uint32_t KK = K > 0 ? (uint32_t)K : (uint32_t)Krt;
-    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int lane = threadIdx.x & 63;
-    const int gl = lane & (G - 1);          // lane within the group
-    const int gbase = lane - gl;            // first lane of the group
-    const int64_t q = q_lo + tid / G;
-    const bool live = q < q_hi;
-    int64_t e0 = 0, cnt = 0;
-    T acc = T(0);
-    if (live) {
-        e0 = rev_ptr[q];
-        cnt = rev_ptr[q + 1] - e0;
-        acc = vbar[q];
-    }
-    for (int64_t base = 0; base < cnt; base += G) {
-        T prod = T(0);
-        if (base + gl < cnt) {
-            const uint32_t c = rev[e0 + base + gl];
-            const uint32_t m = c / KK, j = c - m * KK;
-            prod = mv[(int64_t)j * M + m] * vb[n0 + m];
+    for (int c = sweep_next(ticket, &s_c); c < nchunks; c = sweep_next(ticket, &s_c)) {
+        const int4 ch = chunks[c];
+        if ((int)threadIdx.x >= ch.y) continue;
+        const int64_t q = ch.x + threadIdx.x;
+        const int64_t e0 = rev_ptr[q];
+        const int cnt = (int)(rev_ptr[q + 1] - e0);
+        T acc = vbar[q];
+        for (int base = 0; base < cnt; base += kRevBatch) {
+            int64_t p[kRevBatch];
+            bool live[kRevBatch];
+            T w[kRevBatch], x[kRevBatch];
+#pragma unroll
+            for (int u = 0; u < kRevBatch; ++u) {
+                live[u] = base + u < cnt;
+                const uint32_t e = live[u] ? rev[e0 + base + u] : 0u;
+                const uint32_t m = e / KK, j = e - m * KK;
+                p[u] = n0 + m;
+                w[u] = live[u] ? mv[(int64_t)j * M + m] : T(0);
+            }
+            sweep_read_all<T, kRevBatch>(x, vb, p, live, err);
+#pragma unroll
+            for (int u = 0; u < kRevBatch; ++u)
+                if (live[u]) acc = acc + w[u] * x[u];
         }
-        const int64_t take = cnt - base < G ? cnt - base : G;
-        for (int i = 0; i < take; ++i) acc = acc + __shfl(prod, gbase + i, 64);
-    }
-    if (live && gl == 0) {
-        vb[q] = acc;
+        sweep_publish(vb + q, acc);
         if (xg && q >= n0) xg[q] = sd[q - n0] * acc;
     }
 }
@@ -375,22 +453,25 @@ void PointK<T, K>::pullback(const Graph& g, const Table<T>& tb, int mode, const 
 
 template <typename T, int K>
 void PointK<T, K>::sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                             const T* sd, int64_t m_lo, int64_t len, bool two_pass,
-                             hipStream_t st) {
+                             const T* sd, bool two_pass, hipStream_t st) {
+    const unsigned nwg = (unsigned)std::max(1, std::min(g.n_fwd_chunks, g.sweep_wgs));
     if (two_pass)
-        hipLaunchKernelGGL((k_sweep_fwd<T, K, true>), dim3(grid_for_pt(len)), dim3(kBlock), 0, st,
-                           v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len, (int)g.K);
+        hipLaunchKernelGGL((k_sweep_fwd<T, K, true>), dim3(nwg), dim3(kBlock), 0, st, v, xi,
+                           xi_off, mv, sd, g.nbr, g.M, g.n0, (int)g.K, g.fwd_chunks,
+                           g.n_fwd_chunks, g.sweep_ticket, g.sweep_err);
     else
-        hipLaunchKernelGGL((k_sweep_fwd<T, K, false>), dim3(grid_for_pt(len)), dim3(kBlock), 0,
-                           st, v, xi, xi_off, mv, sd, g.nbr, g.M, g.n0, m_lo, len, (int)g.K);
+        hipLaunchKernelGGL((k_sweep_fwd<T, K, false>), dim3(nwg), dim3(kBlock), 0, st, v, xi,
+                           xi_off, mv, sd, g.nbr, g.M, g.n0, (int)g.K, g.fwd_chunks,
+                           g.n_fwd_chunks, g.sweep_ticket, g.sweep_err);
 }
 
 template <typename T, int K>
 void PointK<T, K>::sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv,
-                             const T* sd, int64_t q_lo, int64_t q_hi, int G, hipStream_t st) {
-    hipLaunchKernelGGL((k_sweep_rev<T, K>), dim3(grid_for_pt((q_hi - q_lo) * G)), dim3(kBlock), 0,
-                       st, vb, vbar, xg, mv, sd, g.rev_ptr, g.rev, g.M, g.n0, q_lo, q_hi, G,
-                       (int)g.K);
+                             const T* sd, hipStream_t st) {
+    const unsigned nwg = (unsigned)std::max(1, std::min(g.n_rev_chunks, g.sweep_wgs));
+    hipLaunchKernelGGL((k_sweep_rev<T, K>), dim3(nwg), dim3(kBlock), 0, st, vb, vbar, xg, mv, sd,
+                       g.rev_ptr, g.rev, g.M, g.n0, (int)g.K, g.rev_chunks, g.n_rev_chunks,
+                       g.sweep_ticket, g.sweep_err);
 }
 
 }  // namespace ggp
