@@ -550,7 +550,7 @@ int op_grad_xi(ggp_graph* h, const T* vbar, T* xbar, hipStream_t user) {
 enum DenseGrad { DG_NONE, DG_LOGDET, DG_GENERATE, DG_INVLOSS };
 
 template <typename T>
-void dense_grad(ggp_graph* h, int kind, hipStream_t st) {
+void dense_grad(ggp_graph* h, int kind, hipStream_t st, bool inverse_ready = false) {
     const Graph& g = h->g;
     const Table<T>& tb = table<T>(h);
     double* rows = h->hist + (size_t)h->nblk_pull * h->hist_nb;
@@ -560,7 +560,7 @@ void dense_grad(ggp_graph* h, int kind, hipStream_t st) {
         dense_grad_logdet<T>(g, tb, tp<T>(h->A), h->W, h->C, rows, h->nw_dense, st);
     } else if (kind == DG_GENERATE) {
         dense_grad_generate<T>(g, tb, tp<T>(h->A), tp<T>(h->vb), tp<T>(h->xt), h->W, h->C, h->Q,
-                               h->u, rows, h->nw_dense, st);
+                               h->u, rows, h->nw_dense, inverse_ready, st);
     } else if (kind == DG_INVLOSS) {
         // xi_dense = L \ y, alpha = L^-T xi_dense (src/dense.jl:229-240).
         T* xid = tp<T>(h->xt);
@@ -598,13 +598,15 @@ int op_grad_vals(ggp_graph* h, int mode, int dkind, const T* in1, const T* in2, 
         dense_factor_async<T>(h, h->s_side);
         dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_side);
         factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr, nullptr);
-        if (int rc = join(h)) return rc;
+        if (int rc = join(h)) return rc;  // the sweeps need v[0:n0]
+        // L^-1 needs only the factor: it runs beside both sweeps
+        dense_inverse<T>(tp<T>(h->A), (int)g.n0, h->W, h->C, h->s_side);
         zero_tail<T>(h, v, h->s_main);
         sweep_forward<T>(h, v, xt, g.n0, h->s_main);
         sweep_reverse<T>(h, vb, vbt, nullptr, h->s_main);
         pull_v = v;
         if (int rc = fork(h)) return rc;
-        dense_grad<T>(h, DG_GENERATE, h->s_side);
+        dense_grad<T>(h, DG_GENERATE, h->s_side, true);
     } else {
         if (mode == P_INVLOSS) {  // inverse loss: values (tree order)
             if (dkind == DG_INVLOSS) {

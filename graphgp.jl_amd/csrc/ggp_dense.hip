@@ -684,11 +684,16 @@ void dense_grad_logdet(const Graph& g, const Table<T>& tb, const T* L, double* W
 // (src/grad_generate_vals.jl:188-211): S = W^T P W with P = Phi(L^T Lbar), P[a][b] = u[a]xi[b]
 // (a > b), u[a]xi[a]/2 (a = b), u = L^T vb; Abar[i][j] = S[i][j] + S[j][i], Abar[j][j] = S[j][j].
 template <typename T>
+void dense_inverse(const T* L, int n, double* W, double* S, hipStream_t st) {
+    dense_inverse64(L, n, W, S, st);
+}
+
+template <typename T>
 void dense_grad_generate(const Graph& g, const Table<T>& tb, const T* L, const T* vb,
                          const T* xi, double* W, double* C, double* Q, double* u,
-                         double* hist_partial, int nw, hipStream_t st) {
+                         double* hist_partial, int nw, bool inverse_ready, hipStream_t st) {
     const int n = (int)g.n0;
-    dense_inverse64(L, n, W, C, st);
+    if (!inverse_ready) dense_inverse64(L, n, W, C, st);
     hipLaunchKernelGGL((k_ltv64<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, L, n, vb, u);
     hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 32)), dim3(256), 0, st, W, n, xi, u, Q);
     launch_gemm<double>({gemm_job(W, n, 1, Q, n, C, n, n, n, n, GK_FROM_I | GK_FROM_J, 1.0)}, st);
@@ -714,7 +719,8 @@ void dense_grad_invloss(const Graph& g, const Table<T>& tb, const T* alpha, doub
                                        double*, double*, int, hipStream_t);                    \
     template void dense_grad_generate<T>(const Graph&, const Table<T>&, const T*, const T*,    \
                                          const T*, double*, double*, double*, double*,         \
-                                         double*, int, hipStream_t);                           \
+                                         double*, int, bool, hipStream_t);                     \
+    template void dense_inverse<T>(const T*, int, double*, double*, hipStream_t);              \
     template void dense_grad_invloss<T>(const Graph&, const Table<T>&, const T*, double*, int, \
                                         hipStream_t);                                          \
     template size_t dense_scatter_lds<T>(const Table<T>&);

@@ -169,10 +169,14 @@ void dense_logdiag(const T* L, int n, double* out, hipStream_t st);
 template <typename T>
 void dense_grad_logdet(const Graph& g, const Table<T>& tb, const T* L, double* W, double* C,
                        double* hist_partial, int nw, hipStream_t st);
+// W = L^-1 (f64, lower); S is n x n scratch.
+template <typename T>
+void dense_inverse(const T* L, int n, double* W, double* S, hipStream_t st);
+// inverse_ready: W already holds L^-1 (dense_inverse ran on this stream or was waited for).
 template <typename T>
 void dense_grad_generate(const Graph& g, const Table<T>& tb, const T* L, const T* vb,
                          const T* xi, double* W, double* C, double* Q, double* u,
-                         double* hist_partial, int nw, hipStream_t st);
+                         double* hist_partial, int nw, bool inverse_ready, hipStream_t st);
 template <typename T>
 void dense_grad_invloss(const Graph& g, const Table<T>& tb, const T* alpha, double* hist_partial,
                         int nw, hipStream_t st);
