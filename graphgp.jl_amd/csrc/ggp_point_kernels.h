@@ -145,9 +145,8 @@ __device__ inline void sweep_read_all(T (&out)[B], const T* p, const int64_t (&i
             atomicOr(err, 4);
             break;
         }
-        if (spins < 4) __builtin_amdgcn_s_sleep(1);
-        else if (spins < 16) __builtin_amdgcn_s_sleep(4);
-        else __builtin_amdgcn_s_sleep(16);
+        if (spins < 8) __builtin_amdgcn_s_sleep(1);
+        else __builtin_amdgcn_s_sleep(4);
 #pragma unroll
         for (int u = 0; u < B; ++u)
             if (b[u] == Pending<T>::bits)
