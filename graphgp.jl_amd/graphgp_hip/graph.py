@@ -1,12 +1,25 @@
-"""build_graph on the host (src/graph_build.jl:254-288) through libggp_graph.so."""
+"""build_graph on the host (src/graph_build.jl:254-288) through libggp_graph.so, and the graph
+interchange format.
+
+The interchange format is the reference's own .npz schema (test/loadref.jl:17-26,
+bench/compare/dump_graph.py:60-70): coords (N, D) uint32 in tree order, neighbors (M, K)
+0-based, offsets (0-based exclusive level ends, offsets[0] = n0), n0, scale, and the covariance
+table as cov_bins32/cov_vals32 or cov_bins64/cov_vals64; this package adds indices (tree
+position -> original position) when the problem has a permutation, and aniso_* keys for an
+anisotropic covariance. A file written by save_graph loads with the reference's load_problem,
+and the reference's fixtures load with load_graph. build_graph(..., cache=path) uses such a file
+as a build cache (the reference's save_graph is Julia serialization only,
+ext/GraphGPMPIExt.jl:176-190).
+"""
 from __future__ import annotations
 
 import ctypes as C
+import os
 
 import numpy as np
 
 from . import _native as nat
-from .problem import GraphGPProblem
+from .problem import AnisoCov, GraphGPProblem
 
 
 def build_graph_arrays(points, n0, k, lattice_bits=21, nthreads=0):
@@ -34,7 +47,64 @@ def build_graph_arrays(points, n0, k, lattice_bits=21, nthreads=0):
     return coords, nbr, offs, nn0.value, scale.value, idx
 
 
-def build_graph(points, n0, k, bins, vals, lattice_bits=21, nthreads=0) -> GraphGPProblem:
-    """GraphGPProblem built from float points (src/graph_build.jl:254-288)."""
-    coords, nbr, offs, nn0, scale, idx = build_graph_arrays(points, n0, k, lattice_bits, nthreads)
-    return GraphGPProblem(coords, nbr, offs, nn0, scale, bins, vals, indices=idx)
+def build_graph(points, n0, k, bins, vals, lattice_bits=21, nthreads=0,
+                cache=None) -> GraphGPProblem:
+    """GraphGPProblem built from float points (src/graph_build.jl:254-288).
+
+    cache: path of an interchange .npz. If it exists and holds a graph of the same N, D, n0 and
+    k, that graph is used (with the given bins/vals); otherwise the graph is built and saved
+    there."""
+    pts = np.asarray(points)
+    if cache is not None and os.path.exists(cache):
+        with np.load(cache, allow_pickle=False) as z:
+            if (z["coords"].shape == pts.shape and int(z["n0"]) == int(n0)
+                    and z["neighbors"].shape[1:] == (int(k),)):
+                idx = z["indices"] if "indices" in z.files else None
+                return GraphGPProblem(z["coords"], z["neighbors"], z["offsets"], int(z["n0"]),
+                                      float(z["scale"]), bins, vals, indices=idx)
+    coords, nbr, offs, nn0, scale, idx = build_graph_arrays(pts, n0, k, lattice_bits, nthreads)
+    prob = GraphGPProblem(coords, nbr, offs, nn0, scale, bins, vals, indices=idx)
+    if cache is not None:
+        save_graph(prob, cache)
+    return prob
+
+
+def save_graph(prob: GraphGPProblem, path) -> None:
+    """Write prob in the interchange schema (uncompressed .npz: loads at memory speed)."""
+    s = "64" if prob.dtype == np.float64 else "32"
+    arrays = dict(coords=prob.coords, neighbors=prob.neighbors, offsets=prob.offsets,
+                  n0=np.int64(prob.n0), scale=np.float64(prob.scale))
+    if prob.cov is None:
+        arrays["cov_bins" + s] = prob.bins
+        arrays["cov_vals" + s] = prob.vals
+    else:
+        arrays.update(aniso_spatial_bins=prob.cov.spatial_bins, aniso_z_bins=prob.cov.z_bins,
+                      aniso_grid=prob.cov.grid, aniso_alpha=np.float64(prob.cov.alpha))
+    if prob.indices is not None:
+        arrays["indices"] = prob.indices
+    tmp = str(path) + ".tmp.npz"
+    np.savez(tmp, **arrays)
+    os.replace(tmp, path)
+
+
+def load_graph(path, dtype=None) -> GraphGPProblem:
+    """Read a graph in the interchange schema (the reference's fixtures included). dtype picks
+    the covariance table when both precisions are stored (default: Float64 if present)."""
+    with np.load(path, allow_pickle=False) as z:
+        files = set(z.files)
+        idx = z["indices"] if "indices" in files else None
+        common = (z["coords"], z["neighbors"], z["offsets"], int(z["n0"]), float(z["scale"]))
+        if "aniso_grid" in files:
+            dt = np.dtype(dtype or z["aniso_grid"].dtype)
+            cov = AnisoCov(z["aniso_spatial_bins"].astype(dt), z["aniso_z_bins"].astype(dt),
+                           z["aniso_grid"].astype(dt), float(z["aniso_alpha"]))
+            return GraphGPProblem(*common, indices=idx, cov=cov)
+        if dtype is None:
+            s = "64" if "cov_bins64" in files else "32"
+        else:
+            s = "64" if np.dtype(dtype) == np.float64 else "32"
+            if "cov_bins" + s not in files:  # convert the stored precision
+                other = "32" if s == "64" else "64"
+                return GraphGPProblem(*common, z["cov_bins" + other].astype(dtype),
+                                      z["cov_vals" + other].astype(dtype), indices=idx)
+        return GraphGPProblem(*common, z["cov_bins" + s], z["cov_vals" + s], indices=idx)

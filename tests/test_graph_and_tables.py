@@ -6,7 +6,8 @@ import numpy as np
 import pytest
 
 import graphgp_hip as G
-from conftest import load_fixture
+from conftest import GOLDEN, load_fixture
+import os
 
 
 @pytest.mark.parametrize("name", ["generate_parity", "aniso_parity"])
@@ -112,3 +113,43 @@ def test_hyperparam_grad_analytic():
     fd = [(np.dot(mk2(var + h, ell)[1], g) - np.dot(mk2(var - h, ell)[1], g)) / (2 * h),
           (np.dot(mk2(var, ell + h)[1], g) - np.dot(mk2(var, ell - h)[1], g)) / (2 * h)]
     np.testing.assert_allclose(got2, fd, rtol=1e-6)
+
+
+def test_interchange_format_round_trip_and_reference_fixtures(tmp_path):
+    """save_graph / load_graph use the reference's .npz schema (test/loadref.jl:17-26): a
+    reference fixture loads to the same arrays the fixture loader builds, a saved graph reloads
+    identically, and build_graph(cache=...) reuses the saved graph."""
+    import graphgp_hip as G
+    z = load_fixture("small")
+    p64 = G.load_graph(os.path.join(GOLDEN, "small.npz"))
+    assert p64.dtype == np.float64
+    np.testing.assert_array_equal(p64.coords, z["coords"])
+    np.testing.assert_array_equal(p64.neighbors, z["neighbors"])
+    np.testing.assert_array_equal(p64.offsets, z["offsets"])
+    np.testing.assert_array_equal(p64.vals, z["cov_vals64"])
+    p32 = G.load_graph(os.path.join(GOLDEN, "small.npz"), dtype=np.float32)
+    np.testing.assert_array_equal(p32.vals, z["cov_vals32"])
+    out = tmp_path / "g.npz"
+    G.save_graph(p32, out)
+    q = G.load_graph(out)
+    for a in ("coords", "neighbors", "offsets", "bins", "vals"):
+        np.testing.assert_array_equal(getattr(q, a), getattr(p32, a))
+    assert q.n0 == p32.n0 and q.scale == p32.scale and q.dtype == np.float32
+    # the build cache
+    rng = np.random.default_rng(4)
+    pts = rng.random((3000, 3))
+    bins, vals = G.rbf_kernel(1.0, 0.1, 1e-4, 2.0, 100)
+    cache = tmp_path / "cache.npz"
+    a = G.build_graph(pts, 100, 8, bins, vals, cache=str(cache))
+    assert cache.exists()
+    b = G.build_graph(pts, 100, 8, bins, vals, cache=str(cache))
+    for f in ("coords", "neighbors", "offsets", "indices"):
+        np.testing.assert_array_equal(getattr(a, f), getattr(b, f))
+    # anisotropic covariance survives the round trip
+    cov = G.AnisoCov(np.linspace(0, 1, 8), np.linspace(0, 0.1, 4), np.ones((8, 4)), 2.0)
+    pa = G.GraphGPProblem(a.coords, a.neighbors, a.offsets, a.n0, a.scale, indices=a.indices,
+                          cov=cov)
+    G.save_graph(pa, tmp_path / "an.npz")
+    qa = G.load_graph(tmp_path / "an.npz")
+    np.testing.assert_array_equal(qa.cov.grid, cov.grid)
+    assert qa.cov.alpha == 2.0
