@@ -693,10 +693,39 @@ int generate_logdet_grad_vals(const Prob& p, T* dvals, double* logdet) {
 }
 
 // ---- src/grad.jl:533-626 (refine_inv_loss_grad_vals, CPU) -----------------------------------
+// Per-point backward of 0.5*xi_m^2 (src/kernels_adjoint.jl:183-211; the same seeds in
+// src/grad.jl:280-300): factor, seed the factor cotangents, Cholesky pullback into s.Abar.
+// Returns xi_m.
+template <typename T>
+T inv_loss_point_pullback(Scratch<T>& s, const Prob& p, int64_t m, const T* values, T scale,
+                          const T* bins, const T* vals) {
+    const int64_t K = p.K, n0 = p.n0, n = s.n;
+    factor_point(s, p, m, scale, bins, vals);
+    mean_vec_solve(s.mv.data(), s.A.data(), K);
+    const T sd = s.A[K * n + K];
+    T mean_val = T(0);
+    for (int64_t j = 0; j < K; ++j) mean_val += s.mv[j] * values[p.neighbors[m * K + j]];
+    const T xi_m = (values[n0 + m] - mean_val) / sd;
+    zero_lbar(s.Lbar.data(), n);
+    s.Lbar[K * n + K] = -xi_m * xi_m / sd;
+    for (int64_t j = 0; j < K; ++j) s.zbar[j] = -xi_m * values[p.neighbors[m * K + j]] / sd;
+    for (int64_t i = 0; i < K; ++i) {
+        T t = s.zbar[i];
+        for (int64_t q = 0; q < i; ++q) t -= s.A[i * n + q] * s.zbar[q];
+        s.zbar[i] = t / s.A[i * n + i];
+    }
+    for (int64_t j = 0; j < K; ++j) {
+        s.Lbar[K * n + j] += s.zbar[j];
+        for (int64_t i = 0; i <= j; ++i) s.Lbar[j * n + i] -= s.zbar[i] * s.mv[j];
+    }
+    chol_pullback_impl<T, false>(s.Abar.data(), s.Lbar.data(), s.A.data(), n);
+    return xi_m;
+}
+
 template <typename T>
 void refine_inv_loss_grad_vals(const Prob& p, const T* values, T* dvals, double* loss) {
     const T* bins = (const T*)p.bins; const T* vals = (const T*)p.vals; const T scale = T(p.scale);
-    const int64_t M = p.N - p.n0, K = p.K, nb = p.nbins, n0 = p.n0;
+    const int64_t M = p.N - p.n0, K = p.K, nb = p.nbins;
     int nch = (int)std::max<int64_t>(1, std::min<int64_t>(p.nthreads, M));
     std::vector<std::vector<T>> dvs(nch, std::vector<T>(p.acc64 ? 0 : nb, T(0)));
     std::vector<std::vector<double>> dvs64(nch, std::vector<double>(p.acc64 ? nb : 0, 0.0));
@@ -706,28 +735,9 @@ void refine_inv_loss_grad_vals(const Prob& p, const T* values, T* dvals, double*
 #pragma omp parallel for num_threads(p.nthreads) schedule(static, 1)
         for (int c = 0; c < nch; ++c) {
             Scratch<T> s(K, p.D);
-            const int64_t n = s.n;
             int64_t lo = c * chunk, hi = std::min<int64_t>(lo + chunk, M);
             for (int64_t m = lo; m < hi; ++m) {
-                factor_point(s, p, m, scale, bins, vals);
-                mean_vec_solve(s.mv.data(), s.A.data(), K);
-                const T sd = s.A[K * n + K];
-                T mean_val = T(0);
-                for (int64_t j = 0; j < K; ++j) mean_val += s.mv[j] * values[p.neighbors[m * K + j]];
-                const T xi_m = (values[n0 + m] - mean_val) / sd;
-                zero_lbar(s.Lbar.data(), n);
-                s.Lbar[K * n + K] = -xi_m * xi_m / sd;
-                for (int64_t j = 0; j < K; ++j) s.zbar[j] = -xi_m * values[p.neighbors[m * K + j]] / sd;
-                for (int64_t i = 0; i < K; ++i) {
-                    T t = s.zbar[i];
-                    for (int64_t q = 0; q < i; ++q) t -= s.A[i * n + q] * s.zbar[q];
-                    s.zbar[i] = t / s.A[i * n + i];
-                }
-                for (int64_t j = 0; j < K; ++j) {
-                    s.Lbar[K * n + j] += s.zbar[j];
-                    for (int64_t i = 0; i <= j; ++i) s.Lbar[j * n + i] -= s.zbar[i] * s.mv[j];
-                }
-                chol_pullback_impl<T, false>(s.Abar.data(), s.Lbar.data(), s.A.data(), n);
+                const T xi_m = inv_loss_point_pullback(s, p, m, values, scale, bins, vals);
                 if (p.acc64) scatter_abar(dvs64[c].data(), s, scale, bins, nb, p.D);
                 else scatter_abar(dvs[c].data(), s, scale, bins, nb, p.D);
                 ls[c] += xi_m * xi_m / T(2);
@@ -886,6 +896,179 @@ int generate_grad_vals(const Prob& p, const T* xi, const T* vbar, T* dvals) {
     return 0;
 }
 
+// ================================ point-position gradients ====================================
+// ---- src/interp.jl:43-60: d cov / d r, the bracketing segment's slope (0 outside the table) --
+template <typename T>
+inline T cov_lookup_dr(T r, const T* bins, const T* vals, int64_t n) {
+    if (r <= bins[0] || r >= bins[n - 1]) return T(0);
+    const int64_t lo = search_lo(r, bins, n);
+    return (vals[lo + 1] - vals[lo]) / (bins[lo + 1] - bins[lo]);
+}
+
+// Off-diagonal cotangent g of the pair (ga, gb) at lattice coordinates (ca, cb) through
+// k'(r) dr/dx into both points (src/grad.jl:205-225): coincident pairs and pairs outside the
+// table's range contribute nothing. dp is point-major (D per point), tree order.
+template <typename T, typename A>
+inline void pair_to_points(A* dp, int64_t ga, int64_t gb, const uint32_t* ca, const uint32_t* cb,
+                           int64_t D, T g, T scale, const T* bins, const T* vals, int64_t nb) {
+    const int64_t sq = sqdist(ca, cb, D);
+    if (sq == 0) return;
+    const T r = std::sqrt(T(sq)) * scale;
+    const T dcov = cov_lookup_dr(r, bins, vals, nb);
+    if (dcov == T(0)) return;
+    const T factor = g * dcov / r;
+    for (int64_t dd = 0; dd < D; ++dd) {
+        const T diff = scale * (T((int64_t)ca[dd]) - T((int64_t)cb[dd]));
+        const T c = factor * diff;
+        dp[ga * D + dd] += (A)c;
+        dp[gb * D + dd] -= (A)c;
+    }
+}
+
+// Abar of one refined point m into its k+1 points.
+template <typename T, typename A>
+inline void scatter_points(A* dp, const Scratch<T>& s, const Prob& p, int64_t m, T scale,
+                           const T* bins, const T* vals) {
+    const int64_t n = s.n, K = p.K, D = p.D;
+    for (int64_t a = 1; a < n; ++a) {
+        const int64_t ga = a < K ? p.neighbors[m * K + a] : p.n0 + m;
+        for (int64_t b = 0; b < a; ++b) {
+            const int64_t gb = b < K ? p.neighbors[m * K + b] : p.n0 + m;
+            pair_to_points(dp, ga, gb, s.jc.data() + a * D, s.jc.data() + b * D, D,
+                           s.Abar[a * n + b], scale, bins, vals, p.nbins);
+        }
+    }
+}
+
+// Serial over the refined points in order, as the reference's host loops; dp (N x D) is summed
+// in T, or in double with acc64.
+template <typename T, typename F>
+void refine_points_loop(const Prob& p, T* dp, F&& seed_pullback) {
+    const T* bins = (const T*)p.bins; const T* vals = (const T*)p.vals; const T scale = T(p.scale);
+    const int64_t M = p.N - p.n0, N = p.N, D = p.D;
+    std::vector<double> dp64(p.acc64 ? N * D : 0, 0.0);
+    for (int64_t i = 0; i < N * D; ++i) dp[i] = T(0);
+    Scratch<T> s(p.K, p.D);
+    for (int64_t m = 0; m < M; ++m) {
+        seed_pullback(s, m, scale, bins, vals);
+        if (p.acc64) scatter_points(dp64.data(), s, p, m, scale, bins, vals);
+        else scatter_points(dp, s, p, m, scale, bins, vals);
+    }
+    if (p.acc64)
+        for (int64_t i = 0; i < N * D; ++i) dp[i] = (T)dp64[i];
+}
+
+// ---- src/grad.jl:168-226 --------------------------------------------------------------------
+template <typename T>
+void refine_logdet_grad_points(const Prob& p, T* dp, double* logdet) {
+    double ld = 0.0;
+    const int64_t K = p.K;
+    refine_points_loop(p, dp, [&](Scratch<T>& s, int64_t m, T scale, const T* bins, const T* vals) {
+        factor_point(s, p, m, scale, bins, vals);
+        const T sd = s.A[K * s.n + K];
+        ld += (double)std::log(sd);
+        zero_lbar(s.Lbar.data(), s.n);
+        s.Lbar[K * s.n + K] = T(1) / sd;  // linalg.jl:140-146, seed 1
+        chol_pullback_impl<T, false>(s.Abar.data(), s.Lbar.data(), s.A.data(), s.n);
+    });
+    if (logdet) *logdet = ld;
+}
+
+// ---- src/grad.jl:239-319 --------------------------------------------------------------------
+template <typename T>
+void refine_inv_loss_grad_points(const Prob& p, const T* values, T* dp, double* loss) {
+    double l = 0.0;
+    refine_points_loop(p, dp, [&](Scratch<T>& s, int64_t m, T scale, const T* bins, const T* vals) {
+        const T xi_m = inv_loss_point_pullback(s, p, m, values, scale, bins, vals);
+        l += (double)(xi_m * xi_m / T(2));
+    });
+    if (loss) *loss = l;
+}
+
+// Dense off-diagonal cotangents G[a][b] (a > b) into the first n0 points (src/dense.jl:185-222,
+// 268-300).
+template <typename T>
+void dense_points_scatter(const Prob& p, const std::vector<T>& G, T* dp) {
+    const T* bins = (const T*)p.bins; const T* vals = (const T*)p.vals; const T scale = T(p.scale);
+    const int64_t n = p.n0, D = p.D;
+    std::vector<double> dp64(p.acc64 ? n * D : 0, 0.0);
+    for (int64_t b = 0; b < n; ++b)
+        for (int64_t a = b + 1; a < n; ++a) {
+            if (p.acc64)
+                pair_to_points(dp64.data(), a, b, p.coords + a * D, p.coords + b * D, D,
+                               G[a * n + b], scale, bins, vals, p.nbins);
+            else
+                pair_to_points(dp, a, b, p.coords + a * D, p.coords + b * D, D, G[a * n + b],
+                               scale, bins, vals, p.nbins);
+        }
+    if (p.acc64)
+        for (int64_t i = 0; i < n * D; ++i) dp[i] += (T)dp64[i];
+}
+
+// ---- src/dense.jl:185-222: cotangent K^-1[a][b] ----------------------------------------------
+template <typename T>
+void dense_logdet_grad_points(const Prob& p, const std::vector<T>& L, T* dp) {
+    const int64_t n = p.n0;
+    std::vector<T> Linv(n * n, T(0)), e(n), col(n), G(n * n, T(0));
+    for (int64_t c = 0; c < n; ++c) {
+        for (int64_t i = 0; i < n; ++i) e[i] = T(i == c ? 1 : 0);
+        trsv_lower(L.data(), n, e.data(), col.data());
+        for (int64_t i = 0; i < n; ++i) Linv[i * n + c] = col[i];
+    }
+    for (int64_t b = 0; b < n; ++b)
+        for (int64_t a = b + 1; a < n; ++a) {
+            T kinv = T(0);
+            for (int64_t kk = 0; kk < n; ++kk) kinv += Linv[kk * n + a] * Linv[kk * n + b];
+            G[a * n + b] = kinv;
+        }
+    dense_points_scatter(p, G, dp);
+}
+
+// ---- src/dense.jl:268-300: cotangent -alpha_a alpha_b, alpha = K^-1 y -------------------------
+template <typename T>
+void dense_inv_loss_grad_points(const Prob& p, const std::vector<T>& L, const T* y, T* dp,
+                                double* loss) {
+    const int64_t n = p.n0;
+    std::vector<T> xi(n), alpha(n), G(n * n, T(0));
+    trsv_lower(L.data(), n, y, xi.data());
+    trsv_lower_t(L.data(), n, xi.data(), alpha.data());
+    for (int64_t b = 0; b < n; ++b)
+        for (int64_t a = b + 1; a < n; ++a) G[a * n + b] = -alpha[a] * alpha[b];
+    dense_points_scatter(p, G, dp);
+    double l = 0.0;
+    for (int64_t i = 0; i < n; ++i) l += 0.5 * (double)xi[i] * (double)xi[i];
+    if (loss) *loss = l;
+}
+
+// ---- src/grad.jl:228-236 --------------------------------------------------------------------
+template <typename T>
+int generate_logdet_grad_points(const Prob& p, T* dp, double* logdet) {
+    double ld_ref = 0.0;
+    refine_logdet_grad_points(p, dp, &ld_ref);
+    std::vector<T> L;
+    if (!dense_factor(p, L)) return 6;
+    dense_logdet_grad_points(p, L, dp);
+    double ld_dense = 0.0;
+    for (int64_t i = 0; i < p.n0; ++i) ld_dense += std::log((double)L[i * p.n0 + i]);
+    if (logdet) *logdet = ld_dense + ld_ref;
+    return 0;
+}
+
+// ---- src/grad.jl:321-336: data in the original order ----------------------------------------
+template <typename T>
+int generate_inv_loss_grad_points(const Prob& p, const T* data, T* dp, double* loss) {
+    const int64_t N = p.N;
+    std::vector<T> d(N);
+    for (int64_t i = 0; i < N; ++i) d[i] = p.indices ? data[p.indices[i]] : data[i];
+    double l_ref = 0.0, l_dense = 0.0;
+    refine_inv_loss_grad_points(p, d.data(), dp, &l_ref);
+    std::vector<T> L;
+    if (!dense_factor(p, L)) return 6;
+    dense_inv_loss_grad_points(p, L, d.data(), dp, &l_dense);
+    if (loss) *loss = l_ref + l_dense;
+    return 0;
+}
+
 }  // namespace
 
 // ================================= C ABI for the tests ========================================
@@ -919,6 +1102,17 @@ int oracle_generate_grad_xi_f32(const ggp_oracle_problem* p, const float* vb, fl
 int oracle_generate_grad_xi_f64(const ggp_oracle_problem* p, const double* vb, double* xb) { return generate_grad_xi<double>(*p, vb, xb); }
 int oracle_generate_grad_vals_f32(const ggp_oracle_problem* p, const float* xi, const float* vb, float* dv) { return generate_grad_vals<float>(*p, xi, vb, dv); }
 int oracle_generate_grad_vals_f64(const ggp_oracle_problem* p, const double* xi, const double* vb, double* dv) { return generate_grad_vals<double>(*p, xi, vb, dv); }
+
+// Point-position gradients exist for the tabulated isotropic covariance only (the reference
+// differentiates cov_lookup in r); an anisotropic problem returns 7.
+int oracle_refine_logdet_grad_points_f32(const ggp_oracle_problem* p, float* dp, double* ld) { if (p->aniso) return 7; refine_logdet_grad_points<float>(*p, dp, ld); return 0; }
+int oracle_refine_logdet_grad_points_f64(const ggp_oracle_problem* p, double* dp, double* ld) { if (p->aniso) return 7; refine_logdet_grad_points<double>(*p, dp, ld); return 0; }
+int oracle_generate_logdet_grad_points_f32(const ggp_oracle_problem* p, float* dp, double* ld) { if (p->aniso) return 7; return generate_logdet_grad_points<float>(*p, dp, ld); }
+int oracle_generate_logdet_grad_points_f64(const ggp_oracle_problem* p, double* dp, double* ld) { if (p->aniso) return 7; return generate_logdet_grad_points<double>(*p, dp, ld); }
+int oracle_refine_inv_loss_grad_points_f32(const ggp_oracle_problem* p, const float* v, float* dp, double* l) { if (p->aniso) return 7; refine_inv_loss_grad_points<float>(*p, v, dp, l); return 0; }
+int oracle_refine_inv_loss_grad_points_f64(const ggp_oracle_problem* p, const double* v, double* dp, double* l) { if (p->aniso) return 7; refine_inv_loss_grad_points<double>(*p, v, dp, l); return 0; }
+int oracle_generate_inv_loss_grad_points_f32(const ggp_oracle_problem* p, const float* d, float* dp, double* l) { if (p->aniso) return 7; return generate_inv_loss_grad_points<float>(*p, d, dp, l); }
+int oracle_generate_inv_loss_grad_points_f64(const ggp_oracle_problem* p, const double* d, double* dp, double* l) { if (p->aniso) return 7; return generate_inv_loss_grad_points<double>(*p, d, dp, l); }
 
 // Primitive-level entry points for the unit tests (single point / single matrix).
 double oracle_cov_lookup_f64(double r, const double* bins, const double* vals, int64_t n) { return cov_lookup<double>(r, bins, vals, n); }

@@ -213,6 +213,26 @@ class Problem:
                    _ptr(self._vec(vbar, self.N)), _ptr(dv))
         return dv
 
+    # ---- point-position gradients, (N, D) in tree order: the memory layout of the reference's
+    # (D, N) Julia matrix ----
+    def _pts(self, name, *vec):
+        dp = np.zeros((self.N, self.D), self.dtype)
+        out = C.c_double()
+        self._call(name, *[_ptr(self._vec(v, self.N)) for v in vec], _ptr(dp), C.byref(out))
+        return out.value, dp
+
+    def refine_logdet_grad_points(self):
+        return self._pts("refine_logdet_grad_points")
+
+    def generate_logdet_grad_points(self):
+        return self._pts("generate_logdet_grad_points")
+
+    def refine_inv_loss_grad_points(self, values_tree):
+        return self._pts("refine_inv_loss_grad_points", values_tree)
+
+    def generate_inv_loss_grad_points(self, data):
+        return self._pts("generate_inv_loss_grad_points", data)
+
     def dense_factor(self):
         L = np.zeros((self.n0, self.n0), self.dtype)
         self._call("dense_factor", _ptr(L))
