@@ -65,6 +65,7 @@ struct ggp_graph {
     double* hist = nullptr;          // (nblk_pull + nw_dense) x nb
     int hist_nb = 0;
     double *W = nullptr, *C = nullptr, *Q = nullptr, *u = nullptr;  // dense f64 scratch (lazy)
+    double *dp = nullptr, *dpd = nullptr;  // d/dpoints accumulators, N x D and n0 x D (lazy)
     std::vector<void*> owned;
     // optional HIP-event timers around the main kernels (ggp_kernel_timers)
     bool timing = false;
@@ -650,6 +651,87 @@ int op_grad_vals(ggp_graph* h, int mode, int dkind, const T* in1, const T* in2, 
     return 0;
 }
 
+// Shared driver of the four d/dpoints ops (src/grad.jl:168-377): the refinement pullback with
+// Abar sent to the point positions (f64 atomics into h->dp), the dense term on the side stream
+// into h->dpd, both rounded once into d_points (N x D, tree order).
+//   mode: P_LOGDET / P_INVLOSS; dense: add the dense first layer.
+template <typename T>
+int op_grad_points(ggp_graph* h, int mode, bool dense, const T* in, T* d_points,
+                   double* scalar_out, hipStream_t user) {
+    if (int rc = check_ready(h)) return rc;
+    if (is_aniso(h))
+        return fail(GGP_ERR_ARG, "gradients w.r.t. the point positions are defined for the "
+                                 "isotropic table only (the anisotropic path is forward-only)");
+    if (!d_points) return fail(GGP_ERR_ARG, "null d_points");
+    if (mode == P_INVLOSS && !in) return fail(GGP_ERR_ARG, "null values");
+    Graph& g = h->g;
+    const int64_t nd = g.N * g.D;
+    if (!h->dp) {
+        if (dmalloc(h, (void**)&h->dp, (size_t)nd * sizeof(double)) ||
+            dmalloc(h, (void**)&h->dpd, (size_t)g.n0 * g.D * sizeof(double)))
+            return GGP_ERR_HIP;
+    }
+    if (dense)
+        if (int rc = ensure_dense64(h)) return rc;
+    if (int rc = enter(h, user)) return rc;
+    const Table<T>& tb = table<T>(h);
+    T* v = tp<T>(h->v);
+    launch_fill<double>(h->dscal, 0.0, 8, h->s_main);
+    launch_fill<int>(h->info, 0, 1, h->s_main);
+    launch_fill<double>(h->dp, 0.0, nd, h->s_main);
+    const T* pull_v = nullptr;
+    if (mode == P_INVLOSS) {
+        if (dense) {  // data in the original order
+            launch_gather<T>(v, in, g.idx, g.N, h->s_main);
+            pull_v = v;
+        } else {
+            pull_v = in;  // values in tree order
+        }
+    }
+    auto dense_part = [&](hipStream_t st) {
+        const int n = (int)g.n0;
+        if (mode == P_LOGDET) {
+            dense_logdiag<T>(tp<T>(h->A), n, h->dscal + 1, st);
+            dense_grad_points_logdet<T>(g, tb, tp<T>(h->A), h->W, h->C, h->dpd, st);
+        } else {
+            // xi_dense = L \ y, alpha = L^-T xi_dense (src/dense.jl:271-300)
+            T* xid = tp<T>(h->xt);
+            T* alpha = tp<T>(h->tmp);
+            dense_trsv<T>(tp<T>(h->A), n, v, xid, st);
+            dense_trsv_t<T>(tp<T>(h->A), n, xid, alpha, st);
+            launch_sumsq_half<T>(xid, n, h->dscal + 1, st);
+            dense_grad_points_invloss<T>(g, tb, alpha, h->dpd, st);
+        }
+    };
+    if (dense) {
+        if (int rc = fork(h)) return rc;
+        dense_factor_async<T>(h, h->s_side);
+        dense_part(h->s_side);
+    }
+    if (g.M > 0) {
+        tstart(h, TM_PULLBACK, h->s_main);
+        launch_pullback<T>(g, tb, mode | P_PTS, pull_v, nullptr, nullptr, h->dp, h->scal_partial,
+                           h->nblk_pull, h->s_main);
+        tstop(h, TM_PULLBACK, h->s_main);
+        launch_reduce_scalar(h->dscal, h->scal_partial, (int)h->nblk_pull, nullptr, h->s_main);
+    }
+    if (dense)
+        if (int rc = join(h)) return rc;
+    const int64_t ndd = dense ? g.n0 * g.D : 0;
+    launch_points_out<T>(d_points, h->dp, h->dpd, nd, ndd, h->s_main);
+    if (int rc = finish(h, user)) return rc;
+    if (dense && *h->hinfo != 0) {
+        if (int rc = dense_retry<T>(h)) return rc;
+        launch_fill<double>(h->dscal + 1, 0.0, 1, h->s_main);
+        dense_part(h->s_main);
+        launch_points_out<T>(d_points, h->dp, h->dpd, nd, ndd, h->s_main);
+        HC(hipMemcpyAsync(h->hscal, h->dscal, 8 * sizeof(double), hipMemcpyDeviceToHost, h->s_main));
+        HC(hipStreamSynchronize(h->s_main));
+    }
+    if (scalar_out) *scalar_out = h->hscal[0] + (dense ? h->hscal[1] : 0.0);
+    return 0;
+}
+
 // ---- graph creation -----------------------------------------------------------------------
 int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const int64_t* offs,
            int64_t n_off, const int64_t* indices, int64_t n0, int64_t k, int64_t N, int32_t D,
@@ -958,6 +1040,29 @@ int ggp_generate_inv_loss_grad_vals(ggp_graph* h, const void* data, void* d_vals
     if (!h) return fail(GGP_ERR_ARG, "null handle");
     return DISPATCH(h, op_grad_vals<float>(h, P_INVLOSS, DG_INVLOSS, (const float*)data, nullptr, (float*)d_vals, loss, ST(stream)),
                     op_grad_vals<double>(h, P_INVLOSS, DG_INVLOSS, (const double*)data, nullptr, (double*)d_vals, loss, ST(stream)));
+}
+
+int ggp_refine_logdet_grad_points(ggp_graph* h, void* d_points, double* logdet, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_grad_points<float>(h, P_LOGDET, false, nullptr, (float*)d_points, logdet, ST(stream)),
+                    op_grad_points<double>(h, P_LOGDET, false, nullptr, (double*)d_points, logdet, ST(stream)));
+}
+int ggp_generate_logdet_grad_points(ggp_graph* h, void* d_points, double* logdet, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_grad_points<float>(h, P_LOGDET, true, nullptr, (float*)d_points, logdet, ST(stream)),
+                    op_grad_points<double>(h, P_LOGDET, true, nullptr, (double*)d_points, logdet, ST(stream)));
+}
+int ggp_refine_inv_loss_grad_points(ggp_graph* h, const void* values_tree, void* d_points,
+                                    double* loss, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_grad_points<float>(h, P_INVLOSS, false, (const float*)values_tree, (float*)d_points, loss, ST(stream)),
+                    op_grad_points<double>(h, P_INVLOSS, false, (const double*)values_tree, (double*)d_points, loss, ST(stream)));
+}
+int ggp_generate_inv_loss_grad_points(ggp_graph* h, const void* data, void* d_points,
+                                      double* loss, void* stream) {
+    if (!h) return fail(GGP_ERR_ARG, "null handle");
+    return DISPATCH(h, op_grad_points<float>(h, P_INVLOSS, true, (const float*)data, (float*)d_points, loss, ST(stream)),
+                    op_grad_points<double>(h, P_INVLOSS, true, (const double*)data, (double*)d_points, loss, ST(stream)));
 }
 
 }  // extern "C"

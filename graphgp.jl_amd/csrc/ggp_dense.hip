@@ -707,6 +707,86 @@ void dense_grad_invloss(const Graph& g, const Table<T>& tb, const T* alpha, doub
     launch_dense_scatter<T, DM_INVLOSS>(g, tb, nullptr, alpha, hist_partial, nw, st);
 }
 
+// ---- d/dpoints of the dense layer (src/dense.jl:185-222, 268-300) -----------------------------
+// One workgroup per point p sums, over every other point q, the pair cotangent G[p][q] through
+// k'(r) dr/dx_p. The reference visits each pair (a > b) once and adds c to a and -c to b; the
+// term p receives from (p, q) is the same c (or its exact negation) evaluated from p's side, so
+// each row is a plain sum and dpd (n x D) is written without atomics.
+// G = K^-1 (C, full symmetric) for the logdet; G = -alpha_p alpha_q for the inverse loss.
+template <typename T, int D, int MODE>
+__global__ void __launch_bounds__(256) k_dense_pts(const uint32_t* __restrict__ coords, int n,
+                                                   T scale, const TabEnt<T>* __restrict__ tab,
+                                                   const uint16_t* __restrict__ acc,
+                                                   const TabParams<T>* __restrict__ Pp,
+                                                   const double* __restrict__ C,
+                                                   const T* __restrict__ alpha,
+                                                   double* __restrict__ dpd) {
+    const TabParams<T> P = *Pp;
+    __shared__ double s_red[4][D];
+    const int p = blockIdx.x;
+    uint32_t cp[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) cp[d] = coords[(int64_t)p * D + d];
+    const T ap = MODE == DM_INVLOSS ? alpha[p] : T(0);
+    double g[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) g[d] = 0.0;
+    for (int q = threadIdx.x; q < n; q += blockDim.x) {
+        if (q == p) continue;
+        uint32_t cq[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) cq[d] = coords[(int64_t)q * D + d];
+        const T gv = MODE == DM_LOGDET ? (T)C[(int64_t)p * n + q] : -ap * alpha[q];
+        T c[D];
+        if (pair_pts<T, D>(cp, cq, gv, scale, tab, acc, P, c)) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) g[d] += (double)c[d];
+        }
+    }
+    const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        double v = g[d];
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o, 64);
+        if (l == 0) s_red[w][d] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < D) {
+        const int d = threadIdx.x;
+        dpd[(int64_t)p * D + d] = s_red[0][d] + s_red[1][d] + s_red[2][d] + s_red[3][d];
+    }
+}
+
+template <typename T, int MODE>
+static void launch_dense_pts(const Graph& g, const Table<T>& tb, const double* C, const T* alpha,
+                             double* dpd, hipStream_t st) {
+    const int n = (int)g.n0;
+    const T scale = (T)g.scale;
+    switch (g.D) {
+        case 2: hipLaunchKernelGGL((k_dense_pts<T, 2, MODE>), dim3(n), dim3(256), 0, st, g.coords, n, scale, tb.tab, tb.acc, tb.params, C, alpha, dpd); break;
+        case 3: hipLaunchKernelGGL((k_dense_pts<T, 3, MODE>), dim3(n), dim3(256), 0, st, g.coords, n, scale, tb.tab, tb.acc, tb.params, C, alpha, dpd); break;
+        case 4: hipLaunchKernelGGL((k_dense_pts<T, 4, MODE>), dim3(n), dim3(256), 0, st, g.coords, n, scale, tb.tab, tb.acc, tb.params, C, alpha, dpd); break;
+        default: break;
+    }
+}
+
+// d(sum log diag L)/dpoints: K^-1 = W^T W in full (both triangles).
+template <typename T>
+void dense_grad_points_logdet(const Graph& g, const Table<T>& tb, const T* L, double* W,
+                              double* C, double* dpd, hipStream_t st) {
+    const int n = (int)g.n0;
+    dense_inverse64(L, n, W, C, st);
+    launch_gemm<double>({gemm_job(W, n, 1, W, n, C, n, n, n, n, GK_FROM_I | GK_FROM_J, 1.0)}, st);
+    launch_dense_pts<T, DM_LOGDET>(g, tb, C, nullptr, dpd, st);
+}
+
+// d(0.5 y^T K^-1 y)/dpoints with alpha = K^-1 y.
+template <typename T>
+void dense_grad_points_invloss(const Graph& g, const Table<T>& tb, const T* alpha, double* dpd,
+                               hipStream_t st) {
+    launch_dense_pts<T, DM_INVLOSS>(g, tb, nullptr, alpha, dpd, st);
+}
+
 #define GGP_DENSE_INST(T)                                                                      \
     template void dense_assemble<T>(const Graph&, const Table<T>&, T*, T, hipStream_t);        \
     template void dense_potrf<T>(T*, int, int*, int*, int, hipStream_t);                                  \
@@ -723,6 +803,10 @@ void dense_grad_invloss(const Graph& g, const Table<T>& tb, const T* alpha, doub
     template void dense_inverse<T>(const T*, int, double*, double*, hipStream_t);              \
     template void dense_grad_invloss<T>(const Graph&, const Table<T>&, const T*, double*, int, \
                                         hipStream_t);                                          \
+    template void dense_grad_points_logdet<T>(const Graph&, const Table<T>&, const T*,         \
+                                              double*, double*, double*, hipStream_t);         \
+    template void dense_grad_points_invloss<T>(const Graph&, const Table<T>&, const T*,        \
+                                               double*, hipStream_t);                          \
     template size_t dense_scatter_lds<T>(const Table<T>&);
 GGP_DENSE_INST(float)
 GGP_DENSE_INST(double)

@@ -49,7 +49,9 @@ struct Table {
 };
 
 enum FactorMode { F_MV = 1, F_TERMS = 2, F_INV = 4 };
-enum PullMode { P_LOGDET = 0, P_INVLOSS = 1, P_GENVALS = 2 };
+// Seeds of the pullback (low two bits); P_PTS sends Abar to the point positions instead of the
+// table histogram (with P_LOGDET or P_INVLOSS).
+enum PullMode { P_LOGDET = 0, P_INVLOSS = 1, P_GENVALS = 2, P_PTS = 4 };
 
 // Launchers of the per-point kernels for one (T, K); defined in ggp_point_kernels.h and
 // instantiated per (T, K) by ggp_inst.hip.
@@ -144,6 +146,10 @@ template <typename T>
 void launch_fill(T* p, T v, int64_t n, hipStream_t st);
 template <typename T>
 void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st);
+// out[i] = dp[i] + dpd[i] (i < n_dense) or dp[i], rounded to T once.
+template <typename T>
+void launch_points_out(T* out, const double* dp, const double* dpd, int64_t n, int64_t n_dense,
+                       hipStream_t st);
 
 // Dense first layer (ggp_dense.hip). Matrices are n x n row-major; L lower.
 template <typename T>
@@ -182,5 +188,12 @@ void dense_grad_invloss(const Graph& g, const Table<T>& tb, const T* alpha, doub
                         int nw, hipStream_t st);
 template <typename T>
 size_t dense_scatter_lds(const Table<T>& tb);
+// d/dpoints of the dense term into dpd (n0 x D, f64, overwritten).
+template <typename T>
+void dense_grad_points_logdet(const Graph& g, const Table<T>& tb, const T* L, double* W,
+                              double* C, double* dpd, hipStream_t st);
+template <typename T>
+void dense_grad_points_invloss(const Graph& g, const Table<T>& tb, const T* alpha, double* dpd,
+                               hipStream_t st);
 
 }  // namespace ggp

@@ -227,6 +227,20 @@ void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st) {
     if (n > 0) hipLaunchKernelGGL((k_copy<T>), dim3(grid_for(n)), dim3(kBlock), 0, st, dst, src, n);
 }
 
+template <typename T>
+__global__ void k_points_out(T* __restrict__ out, const double* __restrict__ dp,
+                             const double* __restrict__ dpd, int64_t n, int64_t n_dense) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = (T)(i < n_dense ? dp[i] + dpd[i] : dp[i]);
+}
+template <typename T>
+void launch_points_out(T* out, const double* dp, const double* dpd, int64_t n, int64_t n_dense,
+                       hipStream_t st) {
+    if (n > 0)
+        hipLaunchKernelGGL((k_points_out<T>), dim3(grid_for(n)), dim3(kBlock), 0, st, out, dp,
+                           dpd, n, n_dense);
+}
+
 #define GGP_INST(T)                                                                            \
     template void launch_factor<T>(const Graph&, const Table<T>&, int, T*, T*, T*, double*,    \
                                    const T*, T*, unsigned, hipStream_t);                       \
@@ -243,7 +257,9 @@ void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st) {
     template void launch_scatter<T>(T*, const T*, const int32_t*, int64_t, hipStream_t);       \
     template void launch_fill<T>(T*, T, int64_t, hipStream_t);                                 \
     template void launch_sumsq_half<T>(const T*, int64_t, double*, hipStream_t);               \
-    template void launch_copy<T>(T*, const T*, int64_t, hipStream_t);
+    template void launch_copy<T>(T*, const T*, int64_t, hipStream_t);                          \
+    template void launch_points_out<T>(T*, const double*, const double*, int64_t, int64_t,     \
+                                       hipStream_t);
 GGP_INST(float)
 GGP_INST(double)
 template void launch_fill<int>(int*, int, int64_t, hipStream_t);

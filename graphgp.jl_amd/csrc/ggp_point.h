@@ -104,6 +104,15 @@ __device__ inline T cov_lookup(T r, const TabEnt<T>* __restrict__ tab,
     return num<T>::fma(e.slope, r - e.x0, e.y0);  // @fastmath y0 + slope*(r - x0)
 }
 
+// cov_lookup_dr (src/interp.jl:43-60): d cov / d r, the bracketing segment's slope; 0 at or
+// beyond either end of the table.
+template <typename T>
+__device__ inline T cov_slope(T r, const TabEnt<T>* __restrict__ tab,
+                              const uint16_t* __restrict__ acc, const TabParams<T>& P) {
+    if (r <= P.b0 || r >= P.bl) return T(0);
+    return tab[seg_index(r, tab, acc, P)].slope;
+}
+
 // cov_lookup_weights (src/interp.jl:62-83): value = wlo*vals[lo] + whi*vals[lo+1].
 template <typename T>
 __device__ inline int cov_weights(T r, const TabEnt<T>* __restrict__ tab,
@@ -137,6 +146,28 @@ __device__ inline double sqdist(const uint32_t (&a)[D], const uint32_t (&b)[D]) 
 template <typename T>
 __device__ inline T radius(double sq, T scale) {
     return num<T>::sqrt((T)sq) * scale;
+}
+
+// One pair's contribution to d/dpoints (src/kernels_adjoint.jl:223-252): the off-diagonal
+// cotangent g of the pair (a, b) through k'(r) dr/dx; c[d] is what point a gains and point b
+// loses. Returns false (c untouched) for coincident points and radii outside the table.
+template <typename T, int D>
+__device__ inline bool pair_pts(const uint32_t (&ca)[D], const uint32_t (&cb)[D], T g, T scale,
+                                const TabEnt<T>* __restrict__ tab,
+                                const uint16_t* __restrict__ acc, const TabParams<T>& P,
+                                T (&c)[D]) {
+    const double sq = sqdist<D>(ca, cb);
+    if (sq == 0.0) return false;
+    const T r = radius<T>(sq, scale);
+    const T dcov = cov_slope(r, tab, acc, P);
+    if (dcov == T(0)) return false;
+    const T f = g * dcov / r;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const T diff = scale * ((T)ca[d] - (T)cb[d]);
+        c[d] = f * diff;
+    }
+    return true;
 }
 
 // ---- anisotropic covariance K(d_spatial, d_z) (src/aniso.jl) ----------------------------------

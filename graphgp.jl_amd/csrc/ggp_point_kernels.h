@@ -295,6 +295,44 @@ __device__ inline void scatter_hist(double* hist, const Block<T, K, D>& blk,
         }
 }
 
+// d/dpoints scatter of one point's Abar (src/kernels_adjoint.jl:223-252): each pair's term is
+// summed per block row in double, then one f64 atomic add per row and coordinate into dp
+// (N x D, tree order).
+template <typename T, int K, int D>
+__device__ inline void scatter_pts(double* dp, const Block<T, K, D>& blk, const int32_t (&nb)[K],
+                                   int64_t m, int64_t n0,
+                                   const T (&Abar)[(K + 1) * (K + 2) / 2], T scale,
+                                   const TabEnt<T>* tab, const uint16_t* acc,
+                                   const TabParams<T>& P) {
+    constexpr int N = K + 1;
+    double g[N][D];
+#pragma unroll
+    for (int a = 0; a < N; ++a)
+#pragma unroll
+        for (int d = 0; d < D; ++d) g[a][d] = 0.0;
+#pragma unroll
+    for (int a = 1; a < N; ++a)
+#pragma unroll
+        for (int b = 0; b < a; ++b) {
+            T c[D];
+            if (pair_pts<T, D>(blk.jc[a], blk.jc[b], Abar[tri(a, b)], scale, tab, acc, P, c)) {
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    g[a][d] += (double)c[d];
+                    g[b][d] -= (double)c[d];
+                }
+            }
+        }
+#pragma unroll
+    for (int a = 0; a < N; ++a) {
+        const int64_t ga = a < K ? (int64_t)nb[a] : n0 + m;
+#pragma unroll
+        for (int d = 0; d < D; ++d) atomicAdd(&dp[ga * D + d], g[a][d]);
+    }
+}
+
+// MODE: P_LOGDET / P_INVLOSS / P_GENVALS seeds the factor cotangents; with P_PTS added, Abar goes
+// to the point positions (hist_partial is then dp, N x D) instead of the table histogram.
 template <typename T, int K, int D, int MODE>
 __global__ void __launch_bounds__(kBlock)
 k_pullback(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, int64_t M,
@@ -304,13 +342,16 @@ k_pullback(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
            const T* __restrict__ xi,    // GENVALS: xi (tree order)
            const T* __restrict__ vb,    // GENVALS: field cotangent after the reverse sweep
            double* __restrict__ hist_partial, double* __restrict__ scalar_partial) {
+    constexpr int SEED = MODE & 3;
+    constexpr bool PTS = (MODE & P_PTS) != 0;
     const TabParams<T> P = *Pp;
     extern __shared__ __align__(16) unsigned char smem[];
     TabEnt<T>* s_tab = reinterpret_cast<TabEnt<T>*>(smem);
     uint16_t* s_acc = reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
     double* s_hist = reinterpret_cast<double*>(smem + tab_bytes<T>(P.nb, P.ucells));
     __shared__ double s_red[kBlock / 64];
-    for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
+    if (!PTS)
+        for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
     stage_table(s_tab, s_acc, g_tab, g_acc, P);
 
     constexpr int N = K + 1;
@@ -327,14 +368,14 @@ k_pullback(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
         T Lbar[NT], Abar[NT];
 #pragma unroll
         for (int i = 0; i < NT; ++i) { Lbar[i] = T(0); Abar[i] = T(0); }
-        if (MODE == P_LOGDET) {
+        if (SEED == P_LOGDET) {
             // src/linalg.jl:140-146 with seed 1; the term itself for the fused logdet.
             ssum += (double)num<T>::log(s);
             Lbar[tri(K, K)] = T(1) / s;
         } else {
             T x[K], zbar[K];
             blk.mean_vec(x);
-            if (MODE == P_INVLOSS) {
+            if (SEED == P_INVLOSS) {
                 // src/kernels_adjoint.jl:183-211 (no @fastmath there).
                 T mean = T(0);
 #pragma unroll
@@ -375,11 +416,16 @@ k_pullback(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
             }
         }
         chol_pullback<T, N>(Abar, Lbar, blk.A);
-        scatter_hist<T, K, D>(s_hist, blk, Abar, scale, s_tab, s_acc, P);
+        if (PTS)
+            scatter_pts<T, K, D>(hist_partial, blk, nb, m, n0, Abar, scale, s_tab, s_acc, P);
+        else
+            scatter_hist<T, K, D>(s_hist, blk, Abar, scale, s_tab, s_acc, P);
     }
     __syncthreads();
-    double* out = hist_partial + (size_t)blockIdx.x * P.nb;
-    for (int i = threadIdx.x; i < P.nb; i += blockDim.x) out[i] = s_hist[i];
+    if (!PTS) {
+        double* out = hist_partial + (size_t)blockIdx.x * P.nb;
+        for (int i = threadIdx.x; i < P.nb; i += blockDim.x) out[i] = s_hist[i];
+    }
     if (scalar_partial) {
         const double t = block_sum(ssum, s_red);
         if (threadIdx.x == 0) scalar_partial[blockIdx.x] = t;
@@ -427,7 +473,8 @@ template <typename T, int K>
 void PointK<T, K>::pullback(const Graph& g, const Table<T>& tb, int mode, const T* v,
                             const T* xi, const T* vb, double* hist_partial,
                             double* scalar_partial, unsigned nblk, hipStream_t st) {
-    const size_t lds = tab_bytes<T>(tb.P.nb, tb.P.ucells) + (size_t)tb.P.nb * sizeof(double);
+    const size_t lds = tab_bytes<T>(tb.P.nb, tb.P.ucells) +
+                       ((mode & P_PTS) ? 0 : (size_t)tb.P.nb * sizeof(double));
     const T scale = (T)g.scale;
 #define GGP_PULL(DD, MODEV)                                                                    \
     hipLaunchKernelGGL((k_pullback<T, K, DD, MODEV>), dim3(nblk), dim3(kBlock), lds, st,        \
@@ -438,6 +485,8 @@ void PointK<T, K>::pullback(const Graph& g, const Table<T>& tb, int mode, const 
         case P_LOGDET: GGP_PULL(DD, P_LOGDET); break;                                          \
         case P_INVLOSS: GGP_PULL(DD, P_INVLOSS); break;                                        \
         case P_GENVALS: GGP_PULL(DD, P_GENVALS); break;                                        \
+        case P_LOGDET | P_PTS: GGP_PULL(DD, P_LOGDET | P_PTS); break;                          \
+        case P_INVLOSS | P_PTS: GGP_PULL(DD, P_INVLOSS | P_PTS); break;                        \
         default: break;                                                                        \
     }
     switch (g.D) {

@@ -35,6 +35,13 @@ __device__ inline void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Sum over the 64 lanes of the wavefront, returned to every lane.
+__device__ inline double wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
 // Joint coordinates of row `lane`: neighbour `lane` for lane < k, the point itself otherwise
 // (_gather_joint!, src/kernels.jl:9-23). Returns the neighbour index (-1 for the point row).
 template <int D>
@@ -195,6 +202,8 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
              const uint16_t* __restrict__ g_acc, const TabParams<T>* __restrict__ Pp,
              const T* __restrict__ v, const T* __restrict__ xi, const T* __restrict__ vb,
              double* __restrict__ hist_partial, double* __restrict__ scalar_partial) {
+    constexpr int SEED = MODE & 3;
+    constexpr bool PTS = (MODE & P_PTS) != 0;
     const TabParams<T> P = *Pp;
     extern __shared__ __align__(16) unsigned char smem[];
     TabEnt<T>* s_tab = reinterpret_cast<TabEnt<T>*>(smem);
@@ -202,7 +211,8 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
     double* s_hist = reinterpret_cast<double*>(smem + tab_bytes<T>(P.nb, P.ucells));
     __shared__ double s_red[kWideWaves];
     __shared__ T s_xch[kWideWaves][2][64];
-    for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
+    if (!PTS)
+        for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
     stage_table(s_tab, s_acc, g_tab, g_acc, P);
 
     const int lane = threadIdx.x & 63;
@@ -225,7 +235,7 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
         // ---- seeds: bc[i] = Lbar[i][lane] ----
 #pragma unroll
         for (int i = 0; i < kWideN; ++i) bc[i] = T(0);
-        if (MODE == P_LOGDET) {
+        if (SEED == P_LOGDET) {
             // src/linalg.jl:140-146 with seed 1; the term itself for the fused logdet.
             if (lane == 0) ssum += (double)num<T>::log(s);
             const T seed = T(1) / s;
@@ -236,7 +246,7 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
             const T xm = wide_mean_vec(a, K, lane);
             const T vnb = lane < K ? v[nb] : T(0);
             T seed, z0;
-            if (MODE == P_INVLOSS) {
+            if (SEED == P_INVLOSS) {
                 // src/kernels_adjoint.jl:183-211 (no @fastmath there).
                 const T prod = lane < K ? xm * vnb : T(0);
                 T mean = T(0);
@@ -265,7 +275,7 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
 #pragma unroll
                     for (int p = 0; p < i; ++p) t = t - bcast(a[p], i) * zs[p];
                     const T dii = bcast(a[i], i);
-                    if (MODE == P_INVLOSS) zs[i] = t / dii;
+                    if (SEED == P_INVLOSS) zs[i] = t / dii;
                     else zs[i] = dii > pivfloor ? t / dii : T(0);
                     zm = lane == i ? zs[i] : zm;
                 }
@@ -285,6 +295,9 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
 
         // ---- chol_pullback! (src/linalg.jl:112-137), columns on lanes ----
         T sbar_mine = T(0);
+        double gpt[D];  // P_PTS: this row's point gradient
+#pragma unroll
+        for (int d = 0; d < D; ++d) gpt[d] = 0.0;
 #pragma unroll
         for (int j = kWideN - 1; j >= 0; --j) {
             if (j < n) {
@@ -302,8 +315,23 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
                 wave_sync();
                 const T tbar = lb / ljj;
                 const T qv = lb * lij / ljj;
-                // Abar[lane][j] = tbar through the lookup weights (src/kernels_adjoint.jl:47-74)
-                {
+                // Abar[lane][j] = tbar through the lookup weights (src/kernels_adjoint.jl:47-74),
+                // or through k'(r) dr/dx into points lane and j (src/kernels_adjoint.jl:223-252)
+                if (PTS) {
+                    uint32_t xj[D];
+#pragma unroll
+                    for (int d = 0; d < D; ++d) xj[d] = bcast(x[d], j);
+                    T c[D];
+#pragma unroll
+                    for (int d = 0; d < D; ++d) c[d] = T(0);
+                    if (row) (void)pair_pts<T, D>(x, xj, tbar, scale, s_tab, s_acc, P, c);
+#pragma unroll
+                    for (int d = 0; d < D; ++d) {
+                        gpt[d] += (double)c[d];
+                        const double cs = wave_sum((double)c[d]);
+                        if (lane == j) gpt[d] -= cs;
+                    }
+                } else {
                     uint32_t xj[D];
 #pragma unroll
                     for (int d = 0; d < D; ++d) xj[d] = bcast(x[d], j);
@@ -330,16 +358,26 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
                 bc[j] = num<T>::fma(-(T(2) * sbar), lc[j], bc[j]);
             }
         }
-        // diagonal of Abar: one add per row into bin 0, summed in row order
-        T diag = T(0);
+        if (PTS) {
+            if (lane < n) {
+                const int64_t gp = lane < K ? (int64_t)nb : n0 + m;
 #pragma unroll
-        for (int j = 0; j < kWideN; ++j)
-            if (j < n) diag += bcast(sbar_mine, j);
-        if (lane == 0) atomicAdd(&s_hist[0], (double)diag);
+                for (int d = 0; d < D; ++d) atomicAdd(&hist_partial[gp * D + d], gpt[d]);
+            }
+        } else {
+            // diagonal of Abar: one add per row into bin 0, summed in row order
+            T diag = T(0);
+#pragma unroll
+            for (int j = 0; j < kWideN; ++j)
+                if (j < n) diag += bcast(sbar_mine, j);
+            if (lane == 0) atomicAdd(&s_hist[0], (double)diag);
+        }
     }
     __syncthreads();
-    double* out = hist_partial + (size_t)blockIdx.x * P.nb;
-    for (int i = threadIdx.x; i < P.nb; i += blockDim.x) out[i] = s_hist[i];
+    if (!PTS) {
+        double* out = hist_partial + (size_t)blockIdx.x * P.nb;
+        for (int i = threadIdx.x; i < P.nb; i += blockDim.x) out[i] = s_hist[i];
+    }
     if (scalar_partial) {
         const double t = block_sum(ssum, s_red);
         if (threadIdx.x == 0) scalar_partial[blockIdx.x] = t;

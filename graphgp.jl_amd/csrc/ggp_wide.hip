@@ -51,7 +51,8 @@ template <typename T, int D>
 void WideD<T, D>::pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, const T* xi,
                         const T* vb, double* hist_partial, double* scalar_partial,
                         unsigned nblk, hipStream_t st) {
-    const size_t lds = tab_bytes<T>(tb.P.nb, tb.P.ucells) + (size_t)tb.P.nb * sizeof(double);
+    const size_t lds = tab_bytes<T>(tb.P.nb, tb.P.ucells) +
+                       ((mode & P_PTS) ? 0 : (size_t)tb.P.nb * sizeof(double));
     const T scale = (T)g.scale;
     const int K = (int)g.K;
     // every one of the nblk histogram rows is written, so the grid stays at nblk
@@ -64,6 +65,8 @@ void WideD<T, D>::pullback(const Graph& g, const Table<T>& tb, int mode, const T
         case P_LOGDET: GGP_PULL_W(DD, P_LOGDET); break;                                        \
         case P_INVLOSS: GGP_PULL_W(DD, P_INVLOSS); break;                                      \
         case P_GENVALS: GGP_PULL_W(DD, P_GENVALS); break;                                      \
+        case P_LOGDET | P_PTS: GGP_PULL_W(DD, P_LOGDET | P_PTS); break;                        \
+        case P_INVLOSS | P_PTS: GGP_PULL_W(DD, P_INVLOSS | P_PTS); break;                      \
         default: break;                                                                        \
     }
     GGP_PULL_W_D(D);

@@ -98,4 +98,23 @@ function generate_logdet_and_grad_vals_hip(hp::HIPProblem{T}) where {T}
     return ld[], dv
 end
 
+# generate_logdet_grad_points (src/grad.jl:242-247): the (D, N) matrix the reference returns is
+# the library's N x D point-major buffer.
+function generate_logdet_grad_points_hip(hp::HIPProblem{T}) where {T}
+    dp = AMDGPU.zeros(T, ndims_space(hp.prob), npoints(hp.prob))
+    _check(ccall(_sym(:ggp_generate_logdet_grad_points), Cint,
+        (Ptr{Cvoid}, Ptr{T}, Ptr{Cdouble}, Ptr{Cvoid}), hp.h, dp, C_NULL, _stream()),
+        "ggp_generate_logdet_grad_points")
+    return dp
+end
+
+# generate_inv_loss_grad_points (src/grad.jl:368-377); data in the original order.
+function generate_inv_loss_grad_points_hip(hp::HIPProblem{T}, data::ROCVector{T}) where {T}
+    dp = AMDGPU.zeros(T, ndims_space(hp.prob), npoints(hp.prob))
+    _check(ccall(_sym(:ggp_generate_inv_loss_grad_points), Cint,
+        (Ptr{Cvoid}, Ptr{T}, Ptr{T}, Ptr{Cdouble}, Ptr{Cvoid}), hp.h, data, dp, C_NULL,
+        _stream()), "ggp_generate_inv_loss_grad_points")
+    return dp
+end
+
 end # module

@@ -18,9 +18,12 @@ from .problem import (
     generate_grad_vals,
     generate_grad_xi,
     generate_inv,
+    generate_inv_loss_grad_points,
     generate_inv_loss_grad_vals,
     generate_logdet,
+    generate_logdet_and_grad_points,
     generate_logdet_and_grad_vals,
+    generate_logdet_grad_points,
     generate_logdet_grad_vals,
     nbins,
     ndims_space,
@@ -29,8 +32,10 @@ from .problem import (
     nrefined,
     refine,
     refine_inv,
+    refine_inv_loss_grad_points,
     refine_inv_loss_grad_vals,
     refine_logdet,
+    refine_logdet_grad_points,
     refine_logdet_grad_vals,
     refine_logdet_terms,
     to_backend,

@@ -64,6 +64,10 @@ _HIP_SIGS = {
     "ggp_generate_logdet_grad_vals": (C.c_int, [_P, _P, _DP, _P]),
     "ggp_refine_inv_loss_grad_vals": (C.c_int, [_P, _P, _P, _DP, _P]),
     "ggp_generate_inv_loss_grad_vals": (C.c_int, [_P, _P, _P, _DP, _P]),
+    "ggp_refine_logdet_grad_points": (C.c_int, [_P, _P, _DP, _P]),
+    "ggp_generate_logdet_grad_points": (C.c_int, [_P, _P, _DP, _P]),
+    "ggp_refine_inv_loss_grad_points": (C.c_int, [_P, _P, _P, _DP, _P]),
+    "ggp_generate_inv_loss_grad_points": (C.c_int, [_P, _P, _P, _DP, _P]),
 }
 
 _GRAPH_SIGS = {

@@ -5,6 +5,12 @@ torch.autograd Functions over the HIP ops:
   logdet_of_vals(prob, vals)               pullback: generate_logdet_grad_vals * ybar
   inv_quadratic_loss_of_vals(prob, vals, data)  pullback: generate_inv_loss_grad_vals * lbar
   generate_of_vals(prob, vals, xi)         pullback: (generate_grad_vals, generate_grad_xi)
+  logdet_of_points(prob, points)           pullback: generate_logdet_grad_points * ybar
+  inv_quadratic_loss_of_points(prob, points, data)  pullback: generate_inv_loss_grad_points * lbar
+
+`points` is the (N, D) tensor of continuous positions in tree order (the reference's (D, N)
+matrix); the forward values use the lattice coordinates and ignore it (straight-through,
+src/chainrules.jl:84-122).
 
 `vals` is a torch tensor (any device); setting it replaces the problem's table, as _set_vals
 does. d/d(data) of the inverse loss is not provided, as in the reference (@not_implemented).
@@ -83,8 +89,42 @@ class _GenerateOfVals(torch.autograd.Function):
         return torch.as_tensor(dvals, dtype=dt, device=dev), dxi, None
 
 
+class _LogdetOfPoints(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, points, prob):
+        ld, g = P.generate_logdet_and_grad_points(prob, as_numpy=False)
+        ctx.save_for_backward(_like(g, points))
+        return torch.tensor(ld, dtype=points.dtype, device=points.device)
+
+    @staticmethod
+    def backward(ctx, ybar):
+        (g,) = ctx.saved_tensors
+        return g * ybar, None
+
+
+class _InvQuadOfPoints(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, points, prob, data):
+        loss, g = P.generate_inv_loss_grad_points(prob, data)
+        ctx.save_for_backward(_like(g, points))
+        return torch.tensor(loss, dtype=points.dtype, device=points.device)
+
+    @staticmethod
+    def backward(ctx, lbar):
+        (g,) = ctx.saved_tensors
+        return g * lbar, None, None
+
+
 def generate(prob, xi):
     return _Generate.apply(xi, prob)
+
+
+def logdet_of_points(prob, points):
+    return _LogdetOfPoints.apply(points, prob)
+
+
+def inv_quadratic_loss_of_points(prob, points, data):
+    return _InvQuadOfPoints.apply(points, prob, data)
 
 
 def logdet_of_vals(prob, vals):

@@ -9,6 +9,8 @@ Reference interface (file:line in the reference):
   refine_logdet_grad_vals ........... src/grad.jl:96-119
   generate_logdet_grad_vals ......... src/grad.jl:149-154 (+ the fused form :680-715)
   refine/generate_inv_loss_grad_vals  src/grad.jl:514-671
+  refine/generate_logdet_grad_points  src/grad.jl:168-247 (dense part src/dense.jl:188-222)
+  refine/generate_inv_loss_grad_points src/grad.jl:259-377 (dense part src/dense.jl:271-300)
   check_graph ....................... src/graph_build.jl:20-57
 
 Conventions are those of the JAX fixtures the reference's tests read (test/loadref.jl): numpy
@@ -386,3 +388,46 @@ def generate_inv_loss_grad_vals(prob, data):
     nat.call("ggp_generate_inv_loss_grad_vals", prob.handle, _ptr(d), _ptr(out), C.byref(loss),
              _stream())
     return loss.value, _out(out, _nb(prob), np_in)
+
+
+# ---- gradients w.r.t. the point positions -------------------------------------------------------
+# Results are (N, D) in tree order: the memory layout of the reference's (D, N) matrix. They are
+# gradients w.r.t. the continuous positions x = scale * coords, the lattice straight-through.
+def _points(prob, fn, vec, as_numpy):
+    _require(prob)
+    args, np_in = [], as_numpy
+    if vec is not None:
+        v, np_in = _dev(vec, prob.N, prob.dtype)
+        args.append(_ptr(v))
+    out = _empty(prob.N * prob.D, prob.dtype)
+    s = C.c_double()
+    nat.call(fn, prob.handle, *args, _ptr(out), C.byref(s), _stream())
+    t = out[: prob.N * prob.D].view(prob.N, prob.D)
+    return s.value, (t.cpu().numpy() if np_in else t)
+
+
+def refine_logdet_grad_points(prob, as_numpy=True):
+    """d(refine_logdet)/dpoints (src/grad.jl:168-226)."""
+    return _points(prob, "ggp_refine_logdet_grad_points", None, as_numpy)[1]
+
+
+def generate_logdet_grad_points(prob, as_numpy=True):
+    """d(generate_logdet)/dpoints, dense + refinement (src/grad.jl:242-247)."""
+    return _points(prob, "ggp_generate_logdet_grad_points", None, as_numpy)[1]
+
+
+def generate_logdet_and_grad_points(prob, as_numpy=True):
+    """(generate_logdet, its d/dpoints) in one pass."""
+    return _points(prob, "ggp_generate_logdet_grad_points", None, as_numpy)
+
+
+def refine_inv_loss_grad_points(prob, values_tree):
+    """(0.5*||refine_inv(values)||^2, its d/dpoints), values in tree order
+    (src/grad.jl:259-319)."""
+    return _points(prob, "ggp_refine_inv_loss_grad_points", values_tree, True)
+
+
+def generate_inv_loss_grad_points(prob, data):
+    """(0.5*||generate_inv(data)||^2, its d/dpoints), data in original order
+    (src/grad.jl:368-377)."""
+    return _points(prob, "ggp_generate_inv_loss_grad_points", data, True)

@@ -141,6 +141,30 @@ int ggp_refine_inv_loss_grad_vals(ggp_graph* h, const void* values_tree, void* d
 int ggp_generate_inv_loss_grad_vals(ggp_graph* h, const void* data, void* d_vals,
                                     double* loss_host, void* stream);
 
+/* ---- gradients w.r.t. the point positions x = scale * coords ------------------------------
+ * d_points is N x D, tree order, point-major: the memory layout of the reference's (D, N)
+ * matrix. Each off-diagonal covariance cotangent reaches the two points through k'(r) dr/dx
+ * (the table's segment slope, 0 outside it); the lattice is straight-through. Isotropic table
+ * only (an anisotropic table returns GGP_ERR_ARG). The scalar (logdet or loss) goes to
+ * *_host when non-NULL. */
+
+/* refine_logdet_grad_points (src/grad.jl:168-226). */
+int ggp_refine_logdet_grad_points(ggp_graph* h, void* d_points, double* logdet_host,
+                                  void* stream);
+
+/* generate_logdet_grad_points (src/grad.jl:242-247; dense part src/dense.jl:188-222). */
+int ggp_generate_logdet_grad_points(ggp_graph* h, void* d_points, double* logdet_host,
+                                    void* stream);
+
+/* refine_inv_loss_grad_points (src/grad.jl:259-319): values_tree is length N, tree order. */
+int ggp_refine_inv_loss_grad_points(ggp_graph* h, const void* values_tree, void* d_points,
+                                    double* loss_host, void* stream);
+
+/* generate_inv_loss_grad_points (src/grad.jl:368-377; dense part src/dense.jl:271-300): data
+ * is length N, original order. */
+int ggp_generate_inv_loss_grad_points(ggp_graph* h, const void* data, void* d_points,
+                                      double* loss_host, void* stream);
+
 /* ---- measurement ------------------------------------------------------------------------- */
 /* No counterpart in the reference (its benchmarks time whole calls, bench/compare/run_julia.jl:50-58).
  * When enabled, each op brackets its main kernels with HIP events on the stream they run on;
