@@ -40,6 +40,8 @@ bool supported_d(int64_t d) { return d >= 2 && d <= 4; }
 
 }  // namespace
 
+int ggp::set_error(int code, const std::string& msg) { return fail(code, msg); }
+
 struct ggp_graph {
     int dtype = GGP_F32;
     int dev = 0;

@@ -14,6 +14,9 @@ constexpr int kBlock = 256;    // threads per workgroup of the per-point kernels
 constexpr int kTile = 32;      // dense-layer tile edge
 constexpr int kWideBlock = 256;  // threads per workgroup of the wavefront-per-point kernels
 
+// Records msg as ggp_last_error() of this thread and returns code.
+int set_error(int code, const std::string& msg);
+
 // Device-resident graph (the reference's GraphGPProblem arrays after to_backend).
 struct Graph {
     int64_t N = 0, n0 = 0, M = 0, K = 0;

@@ -7,7 +7,8 @@ the host-side binding. The rrules live in graphgp_hip.autograd (imported on dema
 """
 from ._native import GraphGPError, build
 from .extras import hyperparam_grad, make_cov_bins, matern_kernel, rbf_kernel
-from .graph import build_graph, build_graph_arrays, load_graph, save_graph
+from .graph import (build_graph, build_graph_arrays, build_graph_device_arrays, load_graph,
+                    save_graph)
 from .problem import (
     AnisoCov,
     GraphGPProblem,

@@ -68,6 +68,8 @@ _HIP_SIGS = {
     "ggp_generate_logdet_grad_points": (C.c_int, [_P, _P, _DP, _P]),
     "ggp_refine_inv_loss_grad_points": (C.c_int, [_P, _P, _P, _DP, _P]),
     "ggp_generate_inv_loss_grad_points": (C.c_int, [_P, _P, _P, _DP, _P]),
+    "ggp_build_graph_device": (C.c_int, [_P, _I64, _I32, _I64, _I64, _I32, _P, _P, _P, _P, _I64,
+                                         C.POINTER(_I64), _DP, _P]),
 }
 
 _GRAPH_SIGS = {

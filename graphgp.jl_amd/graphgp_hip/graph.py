@@ -47,10 +47,41 @@ def build_graph_arrays(points, n0, k, lattice_bits=21, nthreads=0):
     return coords, nbr, offs, nn0.value, scale.value, idx
 
 
+def build_graph_device_arrays(points, n0, k, lattice_bits=21, as_numpy=True):
+    """The graph built on the GPU (ggp_build_graph_device; the role of build_graph_cuda,
+    ext/GraphGPCUDAExt.jl:66-105). Same result as build_graph_arrays. points: (N, D) numpy or a
+    torch tensor on the GPU. Returns (coords, neighbors, offsets, n0, scale, indices); the
+    arrays stay torch GPU tensors when as_numpy is False (offsets are always numpy)."""
+    import torch
+    if isinstance(points, torch.Tensor):
+        pts = points.to(device="cuda", dtype=torch.float64).contiguous()
+    else:
+        pts = torch.from_numpy(np.ascontiguousarray(points, dtype=np.float64)).to("cuda")
+    N, D = pts.shape
+    M = N - int(n0)
+    coords = torch.empty((N, D), dtype=torch.int32, device="cuda")  # uint32 bits
+    nbr = torch.empty((max(M, 1), int(k)), dtype=torch.int64, device="cuda")
+    idx = torch.empty(N, dtype=torch.int64, device="cuda")
+    offs = np.zeros(max(M, 0) + 1, np.int64)
+    n_off, scale = C.c_int64(), C.c_double()
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nat.call("ggp_build_graph_device", C.c_void_p(pts.data_ptr()), N, D, int(n0), int(k),
+             int(lattice_bits), C.c_void_p(coords.data_ptr()), C.c_void_p(nbr.data_ptr()),
+             C.c_void_p(idx.data_ptr()), offs.ctypes.data, len(offs), C.byref(n_off),
+             C.byref(scale), stream)
+    offs = offs[: n_off.value].copy()
+    nbr = nbr[:M]
+    if as_numpy:
+        return (coords.cpu().numpy().view(np.uint32), nbr.cpu().numpy(), offs, int(n0),
+                scale.value, idx.cpu().numpy())
+    return coords, nbr, offs, int(n0), scale.value, idx
+
+
 def build_graph(points, n0, k, bins, vals, lattice_bits=21, nthreads=0,
-                cache=None) -> GraphGPProblem:
+                cache=None, backend="cpu") -> GraphGPProblem:
     """GraphGPProblem built from float points (src/graph_build.jl:254-288).
 
+    backend: "cpu" (the host builder) or "hip" (the same graph built on the GPU).
     cache: path of an interchange .npz. If it exists and holds a graph of the same N, D, n0 and
     k, that graph is used (with the given bins/vals); otherwise the graph is built and saved
     there."""
@@ -62,7 +93,13 @@ def build_graph(points, n0, k, bins, vals, lattice_bits=21, nthreads=0,
                 idx = z["indices"] if "indices" in z.files else None
                 return GraphGPProblem(z["coords"], z["neighbors"], z["offsets"], int(z["n0"]),
                                       float(z["scale"]), bins, vals, indices=idx)
-    coords, nbr, offs, nn0, scale, idx = build_graph_arrays(pts, n0, k, lattice_bits, nthreads)
+    if backend in ("hip", "gpu", "cuda"):
+        coords, nbr, offs, nn0, scale, idx = build_graph_device_arrays(pts, n0, k, lattice_bits)
+    elif backend == "cpu":
+        coords, nbr, offs, nn0, scale, idx = build_graph_arrays(pts, n0, k, lattice_bits,
+                                                                nthreads)
+    else:
+        raise ValueError(f"unknown backend {backend!r}")
     prob = GraphGPProblem(coords, nbr, offs, nn0, scale, bins, vals, indices=idx)
     if cache is not None:
         save_graph(prob, cache)

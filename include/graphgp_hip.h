@@ -165,6 +165,24 @@ int ggp_refine_inv_loss_grad_points(ggp_graph* h, const void* values_tree, void*
 int ggp_generate_inv_loss_grad_points(ggp_graph* h, const void* data, void* d_points,
                                       double* loss_host, void* stream);
 
+/* ---- graph build on the device ----------------------------------------------------------
+ * build_graph (src/graph_build.jl:254-288) on the GPU; replaces gpcuda_build_graph_f32
+ * (csrc/graphgp_capi.cu:100-117, driven by build_graph_cuda, ext/GraphGPCUDAExt.jl:66-105).
+ * Unlike that build (float points, a differently tie-broken tree), this one follows the host
+ * build_graph step for step in double, so it returns the same graph as ggp_build_graph.
+ *   points        device, N*D doubles, point-major, original order
+ *   coords        device, N*D uint32 lattice coordinates, tree order
+ *   neighbors     device, (N-n0)*k int64, 0-based tree positions
+ *   indices       device, N int64, indices[tree_pos] = original_pos
+ *   offsets_host  host, room for offsets_cap level ends (N-n0+1 always suffices);
+ *                 *n_offsets receives the count, *scale the lattice step
+ * 1 <= k <= 32, k <= n0 < N < 2^31, D in 1..4. Synchronous on `stream`; scratch memory is
+ * allocated and released inside the call. Returns 0, GGP_ERR_ARG, GGP_ERR_D or GGP_ERR_HIP. */
+int ggp_build_graph_device(const double* points, int64_t N, int32_t D, int64_t n0, int64_t k,
+                           int32_t lattice_bits, uint32_t* coords, int64_t* neighbors,
+                           int64_t* indices, int64_t* offsets_host, int64_t offsets_cap,
+                           int64_t* n_offsets, double* scale, void* stream);
+
 /* ---- measurement ------------------------------------------------------------------------- */
 /* No counterpart in the reference (its benchmarks time whole calls, bench/compare/run_julia.jl:50-58).
  * When enabled, each op brackets its main kernels with HIP events on the stream they run on;
