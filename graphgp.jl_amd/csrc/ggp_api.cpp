@@ -492,13 +492,26 @@ int op_logdet(ggp_graph* h, bool dense, double* out, hipStream_t user) {
     return 0;
 }
 
+// The refine_* ops take and return tree-order arrays: translate them to the internal order
+// (x_int[i] = x_tree[map[i]]) and back. Without a relabelling (map null) the caller's array is
+// used as is.
+template <typename T>
+const T* tree_in(const T* x, T* buf, const int32_t* map, int64_t n, hipStream_t st) {
+    if (!map) return x;
+    launch_gather<T>(buf, x, map, n, st);
+    return buf;
+}
+
 template <typename T>
 int op_refine_logdet_terms(ggp_graph* h, T* terms, hipStream_t user) {
     if (int rc = check_ready(h)) return rc;
     if (int rc = enter(h, user)) return rc;
-    if (h->g.M > 0)
-        factor_t<T>(h, F_TERMS, nullptr, nullptr, terms, h->scal_partial, nullptr,
-                         nullptr);
+    const Graph& g = h->g;
+    if (g.M > 0) {
+        T* out = g.i2tm ? tp<T>(h->xt) : terms;
+        factor_t<T>(h, F_TERMS, nullptr, nullptr, out, h->scal_partial, nullptr, nullptr);
+        if (g.i2tm) launch_scatter<T>(terms, out, g.i2tm, g.M, h->s_main);
+    }
     return finish(h, user);
 }
 
@@ -506,8 +519,13 @@ template <typename T>
 int op_refine_inv(ggp_graph* h, const T* values, T* xi_ref, hipStream_t user) {
     if (int rc = check_ready(h)) return rc;
     if (int rc = enter(h, user)) return rc;
-    if (h->g.M > 0)
-        factor_t<T>(h, F_INV, nullptr, nullptr, nullptr, nullptr, values, xi_ref);
+    const Graph& g = h->g;
+    if (g.M > 0) {
+        const T* vin = tree_in<T>(values, tp<T>(h->v), g.i2t, g.N, h->s_main);
+        T* out = g.i2tm ? tp<T>(h->xt) : xi_ref;
+        factor_t<T>(h, F_INV, nullptr, nullptr, nullptr, nullptr, vin, out);
+        if (g.i2tm) launch_scatter<T>(xi_ref, out, g.i2tm, g.M, h->s_main);
+    }
     return finish(h, user);
 }
 
@@ -515,10 +533,15 @@ template <typename T>
 int op_refine(ggp_graph* h, T* values, const T* xi_ref, hipStream_t user) {
     if (int rc = check_ready(h)) return rc;
     if (int rc = enter(h, user)) return rc;
-    if (h->g.M > 0) {
+    const Graph& g = h->g;
+    if (g.M > 0) {
+        T* v = g.i2t ? tp<T>(h->v) : values;
+        const T* xr = tree_in<T>(xi_ref, tp<T>(h->xt), g.i2tm, g.M, h->s_main);
+        if (g.i2t) launch_gather<T>(v, values, g.i2t, g.N, h->s_main);
         factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr,
                          nullptr, nullptr);
-        sweep_forward<T>(h, values, xi_ref, 0, h->s_main);
+        sweep_forward<T>(h, v, xr, 0, h->s_main);
+        if (g.i2t) launch_scatter<T>(values, v, g.i2t, g.N, h->s_main);
     }
     return finish(h, user);
 }
@@ -611,12 +634,12 @@ int op_grad_vals(ggp_graph* h, int mode, int dkind, const T* in1, const T* in2, 
         if (int rc = fork(h)) return rc;
         dense_grad<T>(h, DG_GENERATE, h->s_side, true);
     } else {
-        if (mode == P_INVLOSS) {  // inverse loss: values (tree order)
+        if (mode == P_INVLOSS) {  // inverse loss: data (original order) or values (tree order)
             if (dkind == DG_INVLOSS) {
                 launch_gather<T>(v, in1, g.idx, g.N, h->s_main);
                 pull_v = v;
             } else {
-                pull_v = in1;
+                pull_v = tree_in<T>(in1, v, g.i2t, g.N, h->s_main);
             }
         }
         if (dkind != DG_NONE) {
@@ -686,8 +709,8 @@ int op_grad_points(ggp_graph* h, int mode, bool dense, const T* in, T* d_points,
         if (dense) {  // data in the original order
             launch_gather<T>(v, in, g.idx, g.N, h->s_main);
             pull_v = v;
-        } else {
-            pull_v = in;  // values in tree order
+        } else {  // values in tree order
+            pull_v = tree_in<T>(in, v, g.i2t, g.N, h->s_main);
         }
     }
     auto dense_part = [&](hipStream_t st) {
@@ -720,13 +743,13 @@ int op_grad_points(ggp_graph* h, int mode, bool dense, const T* in, T* d_points,
     if (dense)
         if (int rc = join(h)) return rc;
     const int64_t ndd = dense ? g.n0 * g.D : 0;
-    launch_points_out<T>(d_points, h->dp, h->dpd, nd, ndd, h->s_main);
+    launch_points_out<T>(d_points, h->dp, h->dpd, g.N, g.D, ndd, g.i2t, h->s_main);
     if (int rc = finish(h, user)) return rc;
     if (dense && *h->hinfo != 0) {
         if (int rc = dense_retry<T>(h)) return rc;
         launch_fill<double>(h->dscal + 1, 0.0, 1, h->s_main);
         dense_part(h->s_main);
-        launch_points_out<T>(d_points, h->dp, h->dpd, nd, ndd, h->s_main);
+        launch_points_out<T>(d_points, h->dp, h->dpd, g.N, g.D, ndd, g.i2t, h->s_main);
         HC(hipMemcpyAsync(h->hscal, h->dscal, 8 * sizeof(double), hipMemcpyDeviceToHost, h->s_main));
         HC(hipStreamSynchronize(h->s_main));
     }
@@ -808,50 +831,127 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     g.N = N; g.n0 = n0; g.M = M; g.K = k; g.D = D; g.scale = scale;
     g.offsets.assign(offs, offs + n_off);
     const size_t es = dtype == GGP_F32 ? 4 : 8;
-    // neighbours: int32 structure of arrays
+    // Internal order: inside every refined depth level the points are ordered along a Morton
+    // curve of their lattice coordinates, so that the points a chunk of lanes handles are
+    // neighbours in space and their gathers (neighbour coordinates and values, consumers) share
+    // cache lines. The dense block and any points past the last level keep their positions. No
+    // result depends on this order: per-point arithmetic is unchanged and every list keeps the
+    // reference's order; ops translate at their boundary (i2t: internal -> tree position).
+    std::vector<int32_t> i2t((size_t)N), t2i((size_t)N);
+    for (int64_t i = 0; i < N; ++i) i2t[(size_t)i] = (int32_t)i;
+    const bool relabel = M > 0 && !std::getenv("GGP_TREE_ORDER");
+    if (relabel) {
+        uint32_t cmax = 0;
+        for (int64_t i = 0; i < N * D; ++i) cmax = std::max(cmax, coords[i]);
+        int cbits = 0;
+        while (cbits < 32 && (cmax >> cbits) != 0) ++cbits;
+        const int per = 63 / D;
+        const int drop = std::max(0, cbits - per);
+        std::vector<uint64_t> key((size_t)N, 0);
+        for (int64_t i = n0; i < N; ++i) {
+            uint64_t kk = 0;
+            for (int b = per - 1; b >= 0; --b)
+                for (int d = 0; d < D; ++d)
+                    kk = (kk << 1) | ((coords[i * D + d] >> (b + drop)) & 1u);
+            key[(size_t)i] = kk;
+        }
+        for (int64_t b = 1; b < n_off; ++b) {
+            const int64_t lo = offs[b - 1], hi = offs[b];
+            std::stable_sort(i2t.begin() + lo, i2t.begin() + hi,
+                             [&](int32_t a, int32_t c) { return key[(size_t)a] < key[(size_t)c]; });
+        }
+    }
+    for (int64_t i = 0; i < N; ++i) t2i[(size_t)i2t[(size_t)i]] = (int32_t)i;
+    // neighbours: int32 structure of arrays, internal indices
     std::vector<int32_t> nsoa((size_t)(M * k));
-    for (int64_t m = 0; m < M; ++m)
-        for (int64_t j = 0; j < k; ++j) nsoa[(size_t)(j * M + m)] = (int32_t)nbrs[m * k + j];
-    // reverse neighbour list over the points that lie in a level, consumers by decreasing p
+    for (int64_t m = 0; m < M; ++m) {
+        const int64_t mt = i2t[(size_t)(n0 + m)] - n0;  // tree index of internal m
+        for (int64_t j = 0; j < k; ++j)
+            nsoa[(size_t)(j * M + m)] = t2i[(size_t)nbrs[mt * k + j]];
+    }
+    // reverse neighbour list over the points that lie in a level, consumers by decreasing tree
+    // position (entries m*k + j with internal m), indexed by internal q
     const int64_t mlev = std::max<int64_t>(0, offs[n_off - 1] - n0);
     std::vector<int64_t> rptr((size_t)N + 1, 0);
     for (int64_t m = 0; m < mlev; ++m)
-        for (int64_t j = 0; j < k; ++j) rptr[(size_t)nbrs[m * k + j] + 1]++;
+        for (int64_t j = 0; j < k; ++j) rptr[(size_t)t2i[(size_t)nbrs[m * k + j]] + 1]++;
     for (int64_t q = 0; q < N; ++q) rptr[(size_t)q + 1] += rptr[(size_t)q];
-    std::vector<uint32_t> rev((size_t)std::max<int64_t>(rptr[(size_t)N], 1));
+    std::vector<uint32_t> revl((size_t)std::max<int64_t>(rptr[(size_t)N], 1));
     {
         std::vector<int64_t> pos(rptr.begin(), rptr.end() - 1);
-        for (int64_t m = mlev - 1; m >= 0; --m)
+        for (int64_t m = mlev - 1; m >= 0; --m) {
+            const int64_t mi = t2i[(size_t)(n0 + m)] - n0;
             for (int64_t j = 0; j < k; ++j) {
-                const int64_t q = nbrs[m * k + j];
-                rev[(size_t)pos[(size_t)q]++] = (uint32_t)(m * k + j);
+                const int64_t q = t2i[(size_t)nbrs[m * k + j]];
+                revl[(size_t)pos[(size_t)q]++] = (uint32_t)(mi * k + j);
             }
+        }
     }
+    std::vector<uint32_t> rcnt((size_t)N);
+    for (int64_t q = 0; q < N; ++q) rcnt[(size_t)q] = (uint32_t)(rptr[(size_t)q + 1] - rptr[(size_t)q]);
     // Chunk lists of the one-launch sweeps (within one level each, topological order).
     std::vector<int4> fch, rch;
     for (int64_t b = 1; b < n_off; ++b)
         for (int64_t s0 = offs[b - 1]; s0 < offs[b]; s0 += kBlock)
             fch.push_back(make_int4((int)(s0 - n0), (int)std::min<int64_t>(kBlock, offs[b] - s0), 0, 0));
+    // Reverse chunks: the fewest lanes per point (2^lg) that keep every lane at kRevSlots list
+    // entries or fewer (at most 64 lanes; longer lists take several rounds).
+    std::vector<uint32_t> rev;
     for (int64_t b = n_off - 1; b >= 0; --b) {
         const int64_t lo = b == 0 ? 0 : offs[b - 1], hi = b == 0 ? n0 : offs[b];
-        for (int64_t s0 = lo; s0 < hi; s0 += kBlock)
-            rch.push_back(make_int4((int)s0, (int)std::min<int64_t>(kBlock, hi - s0), 0, 0));
+        for (int64_t s0 = lo; s0 < hi;) {
+            int lg = 0;
+            int64_t np = 0, maxc = 0;
+            for (;; ++lg) {
+                np = std::min<int64_t>(kBlock >> lg, hi - s0);
+                maxc = 0;
+                for (int64_t q = s0; q < s0 + np; ++q) maxc = std::max<int64_t>(maxc, rcnt[(size_t)q]);
+                if (((maxc + (1 << lg) - 1) >> lg) <= kRevSlots || lg == 6) break;
+            }
+            const int64_t nslots = (maxc + (1 << lg) - 1) >> lg;
+            const int64_t base = (int64_t)rev.size();
+            if (base + nslots * kBlock >= ((int64_t)1 << 31))
+                return bail(fail(GGP_ERR_ARG, "reverse neighbour lists too large"));
+            rev.resize((size_t)(base + nslots * kBlock), kRevNone);
+            for (int64_t i = 0; i < np; ++i) {
+                const int64_t q = s0 + i;
+                for (int64_t u = 0; u < (int64_t)rcnt[(size_t)q]; ++u) {
+                    const int64_t lane = (i << lg) + (u & ((1 << lg) - 1));
+                    rev[(size_t)(base + (u >> lg) * kBlock + lane)] = revl[(size_t)(rptr[(size_t)q] + u)];
+                }
+            }
+            rch.push_back(make_int4((int)s0, (int)(np | ((int64_t)lg << 16)), (int)base, (int)nslots));
+            s0 += np;
+        }
     }
+    if (rev.empty()) rev.push_back(kRevNone);
     g.n_fwd_chunks = (int)fch.size();
     g.n_rev_chunks = (int)rch.size();
     g.sweep_wgs = h->ncu;
     if (const char* e = std::getenv("GGP_SWEEP_WGS_PER_CU")) g.sweep_wgs = h->ncu * std::max(1, atoi(e));
+    // original position of each internal position
     std::vector<int32_t> idx32;
-    if (indices) {
+    if (indices || relabel) {
         idx32.resize((size_t)N);
-        for (int64_t i = 0; i < N; ++i) idx32[(size_t)i] = (int32_t)indices[i];
+        for (int64_t i = 0; i < N; ++i)
+            idx32[(size_t)i] = indices ? (int32_t)indices[i2t[(size_t)i]] : i2t[(size_t)i];
     }
+    std::vector<uint32_t> coords_int((size_t)(N * D));
+    for (int64_t i = 0; i < N; ++i)
+        for (int d = 0; d < D; ++d)
+            coords_int[(size_t)(i * D + d)] = coords[(int64_t)i2t[(size_t)i] * D + d];
+    std::vector<int32_t> i2tm((size_t)std::max<int64_t>(M, 1));
+    for (int64_t m = 0; m < M; ++m) i2tm[(size_t)m] = i2t[(size_t)(n0 + m)] - (int32_t)n0;
     int rc = 0;
     rc |= dmalloc(h, (void**)&g.coords, (size_t)(N * D) * 4);
     rc |= dmalloc(h, (void**)&g.nbr, nsoa.size() * 4);
-    rc |= dmalloc(h, (void**)&g.rev_ptr, rptr.size() * 8);
+    rc |= dmalloc(h, (void**)&g.rcnt, rcnt.size() * 4);
     rc |= dmalloc(h, (void**)&g.rev, rev.size() * 4);
-    if (indices) rc |= dmalloc(h, (void**)&g.idx, (size_t)N * 4);
+    if (!idx32.empty()) rc |= dmalloc(h, (void**)&g.idx, (size_t)N * 4);
+    if (relabel) {
+        rc |= dmalloc(h, (void**)&g.i2t, (size_t)N * 4);
+        rc |= dmalloc(h, (void**)&g.i2tm, i2tm.size() * 4);
+    }
     rc |= dmalloc(h, &h->mv, (size_t)(M * k) * es);
     rc |= dmalloc(h, &h->sd, (size_t)M * es);
     rc |= dmalloc(h, &h->v, (size_t)N * es);
@@ -873,11 +973,13 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     if (hipHostMalloc((void**)&h->hscal, 8 * 8) != hipSuccess ||
         hipHostMalloc((void**)&h->hinfo, 16) != hipSuccess)
         return bail(fail(GGP_ERR_HIP, "hipHostMalloc failed"));
-    if (hipMemcpy(g.coords, coords, (size_t)(N * D) * 4, hipMemcpyHostToDevice) != hipSuccess ||
+    if (hipMemcpy(g.coords, coords_int.data(), (size_t)(N * D) * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        (relabel && hipMemcpy(g.i2t, i2t.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess) ||
+        (relabel && hipMemcpy(g.i2tm, i2tm.data(), i2tm.size() * 4, hipMemcpyHostToDevice) != hipSuccess) ||
         hipMemcpy(g.nbr, nsoa.data(), nsoa.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(g.rev_ptr, rptr.data(), rptr.size() * 8, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(g.rcnt, rcnt.data(), rcnt.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(g.rev, rev.data(), rev.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        (indices && hipMemcpy(g.idx, idx32.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess) ||
+        (!idx32.empty() && hipMemcpy(g.idx, idx32.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess) ||
         (!fch.empty() && hipMemcpy(g.fwd_chunks, fch.data(), fch.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess) ||
         (!rch.empty() && hipMemcpy(g.rev_chunks, rch.data(), rch.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess) ||
         hipMemset(g.sweep_err, 0, 16) != hipSuccess)

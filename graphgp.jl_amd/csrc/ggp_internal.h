@@ -13,6 +13,8 @@ namespace ggp {
 constexpr int kBlock = 256;    // threads per workgroup of the per-point kernels
 constexpr int kTile = 32;      // dense-layer tile edge
 constexpr int kWideBlock = 256;  // threads per workgroup of the wavefront-per-point kernels
+constexpr int kRevSlots = 16;    // reverse sweep: list entries per lane fetched together
+constexpr uint32_t kRevNone = 0xffffffffu;
 
 // Records msg as ggp_last_error() of this thread and returns code.
 int set_error(int code, const std::string& msg);
@@ -24,13 +26,21 @@ struct Graph {
     double scale = 0;
     uint32_t* coords = nullptr;    // N*D point-major
     int32_t* nbr = nullptr;        // K*M, nbr[j*M + m]
-    int32_t* idx = nullptr;        // N, indices[tree] = orig, or null (identity)
-    int64_t* rev_ptr = nullptr;    // N+1: consumers of point q are rev[rev_ptr[q] .. rev_ptr[q+1])
-    uint32_t* rev = nullptr;       // m*K + j of each consumer, by decreasing consumer position
+    int32_t* idx = nullptr;        // N, original position of each internal position, or null
+    // Internal order = tree order with every refined level sorted along a Morton curve.
+    int32_t* i2t = nullptr;        // N, tree position of each internal position, or null
+    int32_t* i2tm = nullptr;       // M, the same for refined indices (i2t[n0+m] - n0), or null
+    // Consumers of each point (the transpose of the neighbour table), m*K + j each, listed by
+    // decreasing consumer position. rcnt[q] = number of consumers of q. The lists are stored
+    // per reverse-sweep chunk: a point of the chunk uses 2^lg lanes, entry u of its list sits
+    // on lane (i << lg) + (u mod 2^lg) at slot u >> lg, and slot t of lane l is
+    // rev[base + t*kBlock + l] (unused slots hold kRevNone).
+    uint32_t* rcnt = nullptr;      // N
+    uint32_t* rev = nullptr;
     std::vector<int64_t> offsets;  // host copy, offsets[0] = n0
     // Work lists of the one-launch sweeps: chunks of one level each, in topological order.
-    // fwd: {first refined index m, points, 0, 0}; rev: {first position q, points, 0, 0}, latest
-    // level first, the dense block last.
+    // fwd: {first refined index m, points, 0, 0}; rev: {first position q, points | lg << 16,
+    // base, slots}, latest level first, the dense block last.
     int4* fwd_chunks = nullptr;
     int4* rev_chunks = nullptr;
     int n_fwd_chunks = 0, n_rev_chunks = 0;
@@ -149,10 +159,11 @@ template <typename T>
 void launch_fill(T* p, T v, int64_t n, hipStream_t st);
 template <typename T>
 void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st);
-// out[i] = dp[i] + dpd[i] (i < n_dense) or dp[i], rounded to T once.
+// Rows of out (N x D, tree order) = dp (+ dpd on the first n_dense entries), rounded to T
+// once; map: internal -> tree position, or null.
 template <typename T>
-void launch_points_out(T* out, const double* dp, const double* dpd, int64_t n, int64_t n_dense,
-                       hipStream_t st);
+void launch_points_out(T* out, const double* dp, const double* dpd, int64_t N, int D,
+                       int64_t n_dense, const int32_t* map, hipStream_t st);
 
 // Dense first layer (ggp_dense.hip). Matrices are n x n row-major; L lower.
 template <typename T>

@@ -227,18 +227,24 @@ void launch_copy(T* dst, const T* src, int64_t n, hipStream_t st) {
     if (n > 0) hipLaunchKernelGGL((k_copy<T>), dim3(grid_for(n)), dim3(kBlock), 0, st, dst, src, n);
 }
 
+// out[row(r)][d] = dp[r][d] (+ dpd[r][d] for the first n_dense entries), rounded to T once;
+// row = map[r] (internal -> tree position) or r.
 template <typename T>
 __global__ void k_points_out(T* __restrict__ out, const double* __restrict__ dp,
-                             const double* __restrict__ dpd, int64_t n, int64_t n_dense) {
+                             const double* __restrict__ dpd, int64_t N, int D, int64_t n_dense,
+                             const int32_t* __restrict__ map) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = (T)(i < n_dense ? dp[i] + dpd[i] : dp[i]);
+    if (i >= N * D) return;
+    const int64_t r = i / D, d = i - r * D;
+    const int64_t row = map ? (int64_t)map[r] : r;
+    out[row * D + d] = (T)(i < n_dense ? dp[i] + dpd[i] : dp[i]);
 }
 template <typename T>
-void launch_points_out(T* out, const double* dp, const double* dpd, int64_t n, int64_t n_dense,
-                       hipStream_t st) {
-    if (n > 0)
-        hipLaunchKernelGGL((k_points_out<T>), dim3(grid_for(n)), dim3(kBlock), 0, st, out, dp,
-                           dpd, n, n_dense);
+void launch_points_out(T* out, const double* dp, const double* dpd, int64_t N, int D,
+                       int64_t n_dense, const int32_t* map, hipStream_t st) {
+    if (N > 0)
+        hipLaunchKernelGGL((k_points_out<T>), dim3(grid_for(N * D)), dim3(kBlock), 0, st, out, dp,
+                           dpd, N, D, n_dense, map);
 }
 
 #define GGP_INST(T)                                                                            \
@@ -258,8 +264,8 @@ void launch_points_out(T* out, const double* dp, const double* dpd, int64_t n, i
     template void launch_fill<T>(T*, T, int64_t, hipStream_t);                                 \
     template void launch_sumsq_half<T>(const T*, int64_t, double*, hipStream_t);               \
     template void launch_copy<T>(T*, const T*, int64_t, hipStream_t);                          \
-    template void launch_points_out<T>(T*, const double*, const double*, int64_t, int64_t,     \
-                                       hipStream_t);
+    template void launch_points_out<T>(T*, const double*, const double*, int64_t, int,        \
+                                       int64_t, const int32_t*, hipStream_t);
 GGP_INST(float)
 GGP_INST(double)
 template void launch_fill<int>(int*, int, int64_t, hipStream_t);

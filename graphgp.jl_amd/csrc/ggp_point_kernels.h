@@ -156,6 +156,13 @@ __device__ inline void sweep_read_all(T (&out)[B], const T* p, const int64_t (&i
     for (int u = 0; u < B; ++u) out[u] = live[u] ? from_bits(b[u]) : T(0);
 }
 
+// Orders one wavefront's LDS writes before its later reads (no workgroup barrier).
+__device__ inline void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <typename T>
 __device__ inline void sweep_publish(T* p, T x) {
     using U = typename num<T>::bits_t;
@@ -228,45 +235,78 @@ k_sweep_fwd(T* __restrict__ v, const T* __restrict__ xi, int64_t xi_off,
 // Reverse gather (the transpose of the forward apply): vb[q] = vbar[q] + sum over the consumers
 // (p, j) of q of mv_j(p)*vb[p], the consumers listed by decreasing p — exactly the order in
 // which the reference's serial host sweep (src/grad.jl:433-445) adds them — and
-// xg[q] = std_q*vb[q] for refined q. One lane per point; the consumers are fetched kRevBatch at a
-// time (independent loads in flight together) and their products added one by one in list
-// order, which keeps every rounding of the serial sum.
-constexpr int kRevBatch = 8;
+// xg[q] = std_q*vb[q] for refined q.
+// A point feeds about k*ln(N/q) later points, so early levels have long lists and few points.
+// Each chunk therefore gives a point 2^lg lanes (lg chosen per chunk when the graph is built so
+// that a lane holds at most kRevSlots entries): the lanes fetch their entries and the consumer
+// values together (one round trip for the list, one for the values), form the products, and
+// the point's first lane adds them in list order from LDS, which keeps every rounding of the
+// serial sum. The list layout is lane-major per chunk, so every fetch is coalesced. The next
+// chunk's ticket is taken while this one runs.
 template <typename T, int K>
 __global__ void __launch_bounds__(kBlock)
 k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
-            const T* __restrict__ mv, const T* __restrict__ sd,
-            const int64_t* __restrict__ rev_ptr, const uint32_t* __restrict__ rev, int64_t M,
-            int64_t n0, int Krt, const int4* __restrict__ chunks, int nchunks,
-            int* __restrict__ ticket, int* __restrict__ err) {
+            const T* __restrict__ mv, const T* __restrict__ sd, const uint32_t* __restrict__ rcnt,
+            const uint32_t* __restrict__ rev, int64_t M, int64_t n0, int Krt,
+            const int4* __restrict__ chunks, int nchunks, int* __restrict__ ticket,
+            int* __restrict__ err) {
+    constexpr int B = kRevSlots;
     __shared__ int s_c;
+    __shared__ T s_prod[B][kBlock];
+    const int tid = threadIdx.x;
     const uint32_t KK = K > 0 ? (uint32_t)K : (uint32_t)Krt;
-    for (int c = sweep_next(ticket, &s_c); c < nchunks; c = sweep_next(ticket, &s_c)) {
+    if (tid == 0) s_c = atomicAdd(ticket, 1);
+    __syncthreads();
+    int c = __builtin_amdgcn_readfirstlane(s_c);
+    while (c < nchunks) {
         const int4 ch = chunks[c];
-        if ((int)threadIdx.x >= ch.y) continue;
-        const int64_t q = ch.x + threadIdx.x;
-        const int64_t e0 = rev_ptr[q];
-        const int cnt = (int)(rev_ptr[q + 1] - e0);
-        T acc = vbar[q];
-        for (int base = 0; base < cnt; base += kRevBatch) {
-            int64_t p[kRevBatch];
-            bool live[kRevBatch];
-            T w[kRevBatch], x[kRevBatch];
+        __syncthreads();  // every lane has read s_c
+        int next = 0;
+        if (tid == 0) next = atomicAdd(ticket, 1);
+        const int lg = ch.y >> 16, np = ch.y & 0xffff, nslots = ch.w;
+        const int i = tid >> lg, sub = tid & ((1 << lg) - 1);
+        const bool pt = i < np;
+        const int64_t q = (int64_t)ch.x + i;
+        const int cnt = pt ? (int)rcnt[q] : 0;
+        T acc = (pt && sub == 0) ? vbar[q] : T(0);
+        for (int t0 = 0; t0 < nslots; t0 += B) {
+            int64_t p[B];
+            bool live[B];
+            T w[B], x[B];
 #pragma unroll
-            for (int u = 0; u < kRevBatch; ++u) {
-                live[u] = base + u < cnt;
-                const uint32_t e = live[u] ? rev[e0 + base + u] : 0u;
+            for (int u = 0; u < B; ++u) {
+                const int t = t0 + u;
+                live[u] = pt && ((t << lg) + sub) < cnt;
+                const uint32_t e = live[u] ? rev[(int64_t)ch.z + (int64_t)t * kBlock + tid] : 0u;
                 const uint32_t m = e / KK, j = e - m * KK;
                 p[u] = n0 + m;
                 w[u] = live[u] ? mv[(int64_t)j * M + m] : T(0);
             }
-            sweep_read_all<T, kRevBatch>(x, vb, p, live, err);
+            sweep_read_all<T, B>(x, vb, p, live, err);
+            if (lg == 0) {
 #pragma unroll
-            for (int u = 0; u < kRevBatch; ++u)
-                if (live[u]) acc = acc + w[u] * x[u];
+                for (int u = 0; u < B; ++u)
+                    if (live[u]) acc = acc + w[u] * x[u];
+            } else {
+#pragma unroll
+                for (int u = 0; u < B; ++u) s_prod[u][tid] = w[u] * x[u];
+                wave_sync_lds();
+                if (pt && sub == 0) {
+                    const int mask = (1 << lg) - 1;
+                    const int uhi = min(cnt, (t0 + B) << lg);
+                    for (int uu = t0 << lg; uu < uhi; ++uu)
+                        acc = acc + s_prod[(uu >> lg) - t0][(i << lg) + (uu & mask)];
+                }
+                wave_sync_lds();
+            }
         }
-        sweep_publish(vb + q, acc);
-        if (xg && q >= n0) xg[q] = sd[q - n0] * acc;
+        if (pt && sub == 0) {
+            sweep_publish(vb + q, acc);
+            if (xg && q >= n0) xg[q] = sd[q - n0] * acc;
+        }
+        if (tid == 0) s_c = next;
+        __syncthreads();
+        c = __builtin_amdgcn_readfirstlane(s_c);
     }
 }
 
@@ -518,7 +558,7 @@ void PointK<T, K>::sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const 
                              const T* sd, hipStream_t st) {
     const unsigned nwg = (unsigned)std::max(1, std::min(g.n_rev_chunks, g.sweep_wgs));
     hipLaunchKernelGGL((k_sweep_rev<T, K>), dim3(nwg), dim3(kBlock), 0, st, vb, vbar, xg, mv, sd,
-                       g.rev_ptr, g.rev, g.M, g.n0, (int)g.K, g.rev_chunks, g.n_rev_chunks,
+                       g.rcnt, g.rev, g.M, g.n0, (int)g.K, g.rev_chunks, g.n_rev_chunks,
                        g.sweep_ticket, g.sweep_err);
 }
 
