@@ -9,6 +9,7 @@
 // instead of the reference's scalar reverse sweep (src/grad_generate_vals.jl:18-39), which is
 // the same derivative evaluated in a parallel order.
 #include <algorithm>
+#include <cstdlib>
 
 #include "ggp_internal.h"
 
@@ -198,19 +199,362 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_tiles(T* __restrict__ A, i
     }
 }
 
+// ---- the same factor with the diagonal chain kept in one workgroup -----------------------
+// The critical path of the tiled factor is the chain diagonal (j, j) -> sub-diagonal (j+1, j)
+// -> diagonal (j+1, j+1). Above, each link is a different task, so every step pays two
+// cross-workgroup hand-offs (publish, poll, reload). Here the first workgroup to start (ticket
+// 0) is the walker: for every j it factors (j, j) and then solves (j+1, j) itself, keeping
+// L[j][j] and L[j+1][j] in LDS. It starts each tile from a partial sum over k < j-1 that a
+// helper task accumulated one step earlier (in place, flagged), and adds the k = j-1 term
+// itself, so each entry still receives its fma chain in increasing k. The helpers take, by
+// ticket, in column-group order g = 0, 1, ...: the tiles (i, g), i >= g+2 (as above), then the
+// partial sums of (g+2, g+2) and (g+3, g+2) over k < g+1. Every helper task waits only for
+// tasks of earlier groups (or earlier in its own group) and for walker steps <= g, and walker
+// step j waits only for groups <= j-1, so the launch cannot deadlock whatever the residency.
+template <typename T>
+__device__ inline void walk_load(T (&acc)[4], const T* A, int n, int i, int j, int r0, int c) {
+    const int i0 = i * kTile, j0 = j * kTile;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = r0 + 8 * q;
+        acc[q] = (i0 + r < n && j0 + c < n) ? A[(int64_t)(i0 + r) * n + j0 + c]
+                                            : (i == j && r == c ? T(1) : T(0));
+    }
+}
+
+// acc[q] -= X[r0+8q][:] . Y[c][:] over the 32 columns, in column order.
+template <typename T>
+__device__ inline void walk_term(T (&acc)[4], const T (*X)[kTile + 1], const T (*Y)[kTile + 1],
+                                 int r0, int c) {
+#pragma unroll 8
+    for (int p = 0; p < kTile; ++p) {
+        const T lc = Y[c][p];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = num<T>::fma(-X[r0 + 8 * q][p], lc, acc[q]);
+    }
+}
+
+// Terms k in [k0, k1) of tile (i, j) from the published tiles (i, k) and (j, k).
+template <typename T>
+__device__ inline void walk_accumulate(T (&acc)[4], const T* A, int n, int nt, int i, int j,
+                                       int k0, int k1, const int* flags, int* info,
+                                       T (*sA)[kTile + 1], T (*sB)[kTile + 1], int tid, int r0,
+                                       int c) {
+    const int i0 = i * kTile, j0 = j * kTile;
+    for (int k = k0; k < k1; ++k) {
+        if (tid == 0) {
+            df_wait(&flags[i * nt + k], info);
+            if (i != j) df_wait(&flags[j * nt + k], info);
+        }
+        __syncthreads();
+        const int kk = k * kTile;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = r0 + 8 * q;
+            sA[r][c] = i0 + r < n ? A[(int64_t)(i0 + r) * n + kk + c] : T(0);
+            sB[r][c] = j0 + r < n ? A[(int64_t)(j0 + r) * n + kk + c] : T(0);
+        }
+        __syncthreads();
+        walk_term(acc, sA, sB, r0, c);
+        __syncthreads();
+    }
+}
+
+// Solve the tile in sA against L (row r on lane r of wave 0) into global tile (i, j) and, if
+// out is given, into out (LDS). Called by wave 0.
+template <typename T>
+__device__ inline void walk_solve(T* A, int n, int i, int j, const T (*sA)[kTile + 1],
+                                  const T (*L)[kTile + 1], T (*out)[kTile + 1], int tid) {
+    const int r = tid & (kTile - 1);
+    const bool live = tid < kTile && i * kTile + r < n;
+    T a[kTile];
+#pragma unroll
+    for (int cc = 0; cc < kTile; ++cc) a[cc] = sA[r][cc];
+#pragma unroll
+    for (int jj = 0; jj < kTile; ++jj) {
+        T tt = a[jj];
+#pragma unroll
+        for (int p = 0; p < jj; ++p) tt = num<T>::fma(-a[p], L[jj][p], tt);
+        a[jj] = tt / L[jj][jj];
+    }
+    if (live) {
+        T* wp = A + (int64_t)(i * kTile + r) * n + j * kTile;
+#pragma unroll
+        for (int cc = 0; cc < kTile; ++cc) wp[cc] = a[cc];
+    }
+    if (out && tid < kTile)
+#pragma unroll
+        for (int cc = 0; cc < kTile; ++cc) out[r][cc] = a[cc];
+}
+
+__host__ __device__ inline int walk_group_tasks(int g, int nt) {
+    return std::max(0, nt - g - 2) + (g + 2 < nt ? 1 : 0) + (g + 3 < nt ? 1 : 0);
+}
+
+constexpr int kLtPitch = kTile + 4;  // transposed L rows, 16-byte aligned
+
+// Walker factor of the tile in sA into global tile (j, j) and, transposed, into Lt (LDS; zero
+// above the diagonal). Right-looking by columns: lane r owns row r; at step p the pivot and the
+// column values come from their lanes by readlane, and every entry (r, c), c > p, takes
+// fma(-L[r][p], L[c][p], .) — the unblocked left-looking chain in its order. Entries above the
+// diagonal are scratch (updated, never stored). Called by wave 0.
+template <typename T>
+__device__ inline void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1],
+                                     T (*Lt)[kLtPitch], int tid, int* info) {
+    const int r = tid & (kTile - 1);
+    const bool live = tid < kTile && j * kTile + r < n;
+    T a[kTile];
+#pragma unroll
+    for (int cc = 0; cc < kTile; ++cc) a[cc] = sA[r][cc];
+    bool bad = false;
+#pragma unroll
+    for (int p = 0; p < kTile; ++p) {
+        const T piv = bcast(a[p], p);
+        bad = bad || !(piv > T(0));
+        const T d = num<T>::sqrt(piv);
+        const T l = a[p] / d;
+        a[p] = r == p ? d : l;
+#pragma unroll
+        for (int cc = p + 1; cc < kTile; ++cc) a[cc] = num<T>::fma(-a[p], bcast(a[p], cc), a[cc]);
+    }
+    if (live) {
+        T* wp = A + (int64_t)(j * kTile + r) * n + j * kTile;
+#pragma unroll
+        for (int cc = 0; cc < kTile; ++cc)
+            if (cc <= r) wp[cc] = a[cc];
+    }
+    if (tid < kTile)
+#pragma unroll
+        for (int cc = 0; cc < kTile; ++cc) Lt[cc][r] = cc <= r ? a[cc] : T(0);
+    if (tid == 0 && bad) atomicOr(info, 1);
+}
+
+// Walker solve of X L^T = B (B in sC) by columns: step p divides column p by L[p][p] and folds
+// it into the later columns, so entry (r, c) receives fma(-x[r][p], L[c][p], .) for p = 0, 1,
+// ... and then its division: the row-by-row substitution's chain, in its order. Wave 0; lane
+// 32h + r holds row r, columns 16h .. 16h+15, so both halves of the wavefront share the
+// updates; column p of L is a row of Lt (LDS broadcast). The result goes to global tile (i, j)
+// and to P.
+template <typename T>
+__device__ inline void walk_solve_t(T* A, int n, int i, int j, const T (*sC)[kTile + 1],
+                                    const T (*Lt)[kLtPitch], T (*P)[kTile + 1], int tid) {
+    const int r = tid & (kTile - 1), h = tid >> 5;
+    T a[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) a[u] = sC[r][16 * h + u];
+#pragma unroll
+    for (int p = 0; p < kTile; ++p) {
+        const int hp = p >> 4, up = p & 15;
+        const T x = a[up] / Lt[p][p];
+        const bool mine = h == hp;
+        a[up] = mine ? x : a[up];
+        const T xo = __shfl_xor(x, 32, 64);
+        const T xp = mine ? x : xo;
+        const T* lrow = &Lt[p][16 * h];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            // columns past p only: u > p in half 0, u + 16 > p in half 1
+            if (u + 16 > p) {
+                const T y = num<T>::fma(-xp, lrow[u], a[u]);
+                a[u] = (u > p || h == 1) ? y : a[u];
+            }
+        }
+    }
+    if (i * kTile + r < n) {
+        T* wp = A + (int64_t)(i * kTile + r) * n + j * kTile + 16 * h;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) wp[u] = a[u];
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) P[r][16 * h + u] = a[u];
+}
+
+// Rows [R, R+16) of tile (i, j) for a 64-lane wavefront: lane l holds (R + (l >> 5) + 2q, l & 31).
+template <typename T>
+__device__ inline void walk_load16(T (&v)[8], const T* A, int n, int i, int j, int R, int lane) {
+    const int c = lane & (kTile - 1), rr = lane >> 5;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int r = R + rr + 2 * q;
+        v[q] = (i * kTile + r < n && j * kTile + c < n) ? A[(int64_t)(i * kTile + r) * n + j * kTile + c]
+                                                          : (i == j && r == c ? T(1) : T(0));
+    }
+}
+
+// sync = [ticket, tile flags[nt*nt], diagonal-partial flags[nt], sub-diagonal-partial flags[nt]]
+template <typename T>
+__global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, int n, int nt,
+                                                           int ntasks, int* __restrict__ sync,
+                                                           int* __restrict__ info) {
+    __shared__ T sA[kTile][kTile + 1];
+    __shared__ T sB[kTile][kTile + 1];
+    __shared__ T sC[kTile][kTile + 1];
+    __shared__ T sP[kTile][kTile + 1];            // walker: L[j][j-1], then L[j+1][j]
+    __shared__ __align__(16) T sLt[kTile][kLtPitch];  // walker: L[j][j] transposed
+    __shared__ int s_task;
+    int* ticket = sync;
+    int* flags = sync + 1;
+    int* pdf = flags + nt * nt;
+    int* psf = pdf + nt;
+    const int tid = threadIdx.x;
+    const int c = tid & (kTile - 1), r0 = tid >> 5;
+    if (tid == 0) s_task = atomicAdd(ticket, 1);
+    __syncthreads();
+    int t = __builtin_amdgcn_readfirstlane(s_task);
+    if (t == 0) {
+        // ---- the walker ----
+        // Wave 0 factors and solves; waves 1 and 2 (rows 0-15 and 16-31) meanwhile prepare the
+        // next sub-diagonal tile and the next diagonal partial sum. The walker is the critical
+        // path and shares its CU with the concurrent per-point kernels: its waves take issue
+        // priority on their SIMDs.
+        __builtin_amdgcn_s_setprio(3);
+        const int w = tid >> 6, lane = tid & 63;
+        {
+            T v[4];
+            walk_load(v, A, n, 0, 0, r0, c);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sA[r0 + 8 * q][c] = v[q];
+        }
+        __syncthreads();
+        for (int j = 0; j < nt; ++j) {
+            const bool sub = j + 1 < nt;
+            // diagonal tile: partial sum (in sA) plus the k = j-1 term
+            T acc[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[q] = sA[r0 + 8 * q][c];
+            if (j >= 1) walk_term(acc, sP, sP, r0, c);
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sA[r0 + 8 * q][c] = acc[q];
+            __syncthreads();
+            if (w == 0) {
+                walk_factor_t(A, n, j, sA, sLt, tid, info);
+            } else if (sub && w <= 2) {
+                // sub-diagonal tile: partial sum over k < j-1 plus the k = j-1 term, into sC
+                const int R = 16 * (w - 1);
+                if (lane == 0) {
+                    if (j >= 2) df_wait(&psf[j], info);
+                    if (j >= 1) df_wait(&flags[(j + 1) * nt + j - 1], info);
+                }
+                T nx[8];
+                walk_load16(nx, A, n, j + 1, j, R, lane);
+                if (j >= 1) {
+                    T lo[8];
+                    walk_load16(lo, A, n, j + 1, j - 1, R, lane);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) sB[R + (lane >> 5) + 2 * q][lane & 31] = lo[q];
+                    wave_sync_lds();
+#pragma unroll 8
+                    for (int p = 0; p < kTile; ++p) {
+                        const T lc = sP[lane & 31][p];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q)
+                            nx[q] = num<T>::fma(-sB[R + (lane >> 5) + 2 * q][p], lc, nx[q]);
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) sC[R + (lane >> 5) + 2 * q][lane & 31] = nx[q];
+            }
+            __syncthreads();
+            if (tid == 0)
+                __hip_atomic_store(&flags[j * nt + j], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            if (sub) {
+                if (w == 0) {
+                    walk_solve_t(A, n, j + 1, j, sC, sLt, sP, tid);
+                } else if (w <= 2) {
+                    // next diagonal partial sum into sA
+                    const int R = 16 * (w - 1);
+                    if (lane == 0 && j + 1 >= 2) df_wait(&pdf[j + 1], info);
+                    T v[8];
+                    walk_load16(v, A, n, j + 1, j + 1, R, lane);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) sA[R + (lane >> 5) + 2 * q][lane & 31] = v[q];
+                }
+                __syncthreads();
+                if (tid == 0)
+                    __hip_atomic_store(&flags[(j + 1) * nt + j], 1, __ATOMIC_RELEASE,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        return;
+    }
+    // ---- helpers ----
+    t -= 1;
+    while (t < ntasks) {
+        __syncthreads();
+        int g = 0, rem = t;
+        while (rem >= walk_group_tasks(g, nt)) { rem -= walk_group_tasks(g, nt); ++g; }
+        const int nreg = std::max(0, nt - g - 2);
+        T acc[4];
+        if (rem < nreg) {
+            // tile (i, g), i >= g+2: all terms, then the solve against L[g][g]
+            const int i = g + 2 + rem;
+            walk_load(acc, A, n, i, g, r0, c);
+            walk_accumulate(acc, A, n, nt, i, g, 0, g, flags, info, sA, sB, tid, r0, c);
+            if (tid == 0) df_wait(&flags[g * nt + g], info);
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = r0 + 8 * q;
+                sA[r][c] = acc[q];
+                sB[r][c] = (g * kTile + r < n && c <= r) ? A[(int64_t)(g * kTile + r) * n + g * kTile + c] : T(0);
+            }
+            __syncthreads();
+            if (tid < 64) walk_solve(A, n, i, g, sA, sB, (T(*)[kTile + 1])nullptr, tid);
+            __syncthreads();
+            if (tid == 0) {
+                __hip_atomic_store(&flags[i * nt + g], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                s_task = atomicAdd(ticket, 1);
+            }
+        } else {
+            // partial sum over k < g+1 of the walker's tile (d, d) or (d+1, d), d = g+2
+            const int d = g + 2;
+            const bool diag = rem == nreg;
+            const int i = diag ? d : d + 1;
+            walk_load(acc, A, n, i, d, r0, c);
+            walk_accumulate(acc, A, n, nt, i, d, 0, d - 1, flags, info, sA, sB, tid, r0, c);
+            // (the diagonal tile keeps its upper triangle, which no one reads)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = r0 + 8 * q;
+                if (i * kTile + r < n && d * kTile + c < n && (!diag || c <= r))
+                    A[(int64_t)(i * kTile + r) * n + d * kTile + c] = acc[q];
+            }
+            __syncthreads();
+            if (tid == 0) {
+                __hip_atomic_store(diag ? &pdf[d] : &psf[d], 1, __ATOMIC_RELEASE,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                s_task = atomicAdd(ticket, 1);
+            }
+        }
+        __syncthreads();
+        t = __builtin_amdgcn_readfirstlane(s_task) - 1;
+    }
+}
+
 int dense_sync_ints(int n) {
     const int nt = (n + kTile - 1) / kTile;
-    return nt * nt + 1;
+    return nt * nt + 2 * nt + 1;
 }
 
 template <typename T>
 void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st) {
     if (n <= 0) return;
     const int nt = (n + kTile - 1) / kTile;
-    const int ntiles = nt * (nt + 1) / 2;
     launch_fill<int>(sync, 0, dense_sync_ints(n), st);
-    const int nwg = std::max(1, std::min(ntiles, max_wg));
-    hipLaunchKernelGGL((k_potrf_tiles<T>), dim3(nwg), dim3(kDfThreads), 0, st, A, n, nt, sync, info);
+    static const bool tiles = std::getenv("GGP_POTRF_TILES") != nullptr;
+    if (tiles) {
+        const int ntiles = nt * (nt + 1) / 2;
+        const int nwg = std::max(1, std::min(ntiles, max_wg));
+        hipLaunchKernelGGL((k_potrf_tiles<T>), dim3(nwg), dim3(kDfThreads), 0, st, A, n, nt, sync,
+                           info);
+        return;
+    }
+    int ntasks = 0;
+    for (int g = 0; g < nt; ++g) ntasks += walk_group_tasks(g, nt);
+    const int nwg = std::max(1, std::min(ntasks + 1, max_wg));
+    hipLaunchKernelGGL((k_potrf_walk<T>), dim3(nwg), dim3(kDfThreads), 0, st, A, n, nt, ntasks,
+                       sync, info);
 }
 
 // ---- triangular products and solves ---------------------------------------------------------

@@ -56,6 +56,13 @@ __device__ inline T put(T x, T v, int lane, int me) {
     return me == lane ? v : x;
 }
 
+// Orders one wavefront's LDS writes before its later reads (no workgroup barrier).
+__device__ inline void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Index of (i, j), i >= j, in a packed lower triangle.
 __host__ __device__ constexpr int tri(int i, int j) { return i * (i + 1) / 2 + j; }
 

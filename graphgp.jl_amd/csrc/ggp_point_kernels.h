@@ -156,13 +156,6 @@ __device__ inline void sweep_read_all(T (&out)[B], const T* p, const int64_t (&i
     for (int u = 0; u < B; ++u) out[u] = live[u] ? from_bits(b[u]) : T(0);
 }
 
-// Orders one wavefront's LDS writes before its later reads (no workgroup barrier).
-__device__ inline void wave_sync_lds() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 template <typename T>
 __device__ inline void sweep_publish(T* p, T x) {
     using U = typename num<T>::bits_t;
