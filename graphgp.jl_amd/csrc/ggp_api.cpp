@@ -387,21 +387,23 @@ int check_ready(ggp_graph* h) {
 // Forward sweep over all depth levels (src/api.jl:126-137), one launch; xi indexed as
 // xi[xi_off + m].
 template <typename T>
-void sweep_forward(ggp_graph* h, T* v, const T* xi, int64_t xi_off, hipStream_t st) {
+void sweep_forward(ggp_graph* h, T* v, const T* xi, int64_t xi_off, hipStream_t st,
+                   bool prepared = false) {
     const Graph& g = h->g;
     tstart(h, TM_SWEEP_FWD, st);
     launch_sweep_fwd<T>(g, v, xi, xi_off, tp<T>(h->mv), tp<T>(h->sd),
-                        table<T>(h).aniso.grid != nullptr, st);
+                        table<T>(h).aniso.grid != nullptr, prepared, st);
     tstop(h, TM_SWEEP_FWD, st);
 }
 
 // Reverse sweep, latest level first, then the dense level (src/grad.jl:433-445, 483-489), one
 // launch.
 template <typename T>
-void sweep_reverse(ggp_graph* h, T* vb, const T* vbar, T* xg, hipStream_t st) {
+void sweep_reverse(ggp_graph* h, T* vb, const T* vbar, T* xg, hipStream_t st,
+                   bool prepared = false) {
     const Graph& g = h->g;
     tstart(h, TM_SWEEP_REV, st);
-    launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), st);
+    launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), prepared, st);
     tstop(h, TM_SWEEP_REV, st);
 }
 
@@ -419,14 +421,17 @@ int op_generate(ggp_graph* h, const T* xi, T* out, hipStream_t user) {
     if (int rc = enter(h, user)) return rc;
     Graph& g = h->g;
     T *xt = tp<T>(h->xt), *v = tp<T>(h->v);
-    launch_gather<T>(xt, xi, g.idx, g.N, h->s_main);
+    // the dense factor is the longest chain: start it first; everything else on the main
+    // stream overlaps it
     if (int rc = fork(h)) return rc;
     dense_factor_async<T>(h, h->s_side);
-    dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_side);
+    launch_gather<T>(xt, xi, g.idx, g.N, h->s_main);
+    launch_sweep_prep<T>(g, v, nullptr, h->s_main);
+    zero_tail<T>(h, v, h->s_main);
     factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr, nullptr);
     if (int rc = join(h)) return rc;
-    zero_tail<T>(h, v, h->s_main);
-    sweep_forward<T>(h, v, xt, g.n0, h->s_main);
+    dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_main);
+    sweep_forward<T>(h, v, xt, g.n0, h->s_main, true);
     launch_scatter<T>(out, v, g.idx, g.N, h->s_main);
     if (int rc = finish(h, user)) return rc;
     if (*h->hinfo != 0) {
@@ -445,12 +450,12 @@ int op_generate_inv(ggp_graph* h, const T* values, T* xi_out, hipStream_t user) 
     if (int rc = enter(h, user)) return rc;
     Graph& g = h->g;
     T *vt = tp<T>(h->v), *xt = tp<T>(h->xt);
-    launch_gather<T>(vt, values, g.idx, g.N, h->s_main);
     if (int rc = fork(h)) return rc;
     dense_factor_async<T>(h, h->s_side);
-    dense_trsv<T>(tp<T>(h->A), (int)g.n0, vt, xt, h->s_side);
+    launch_gather<T>(vt, values, g.idx, g.N, h->s_main);
     factor_t<T>(h, F_INV, nullptr, nullptr, nullptr, nullptr, vt, xt + g.n0);
     if (int rc = join(h)) return rc;
+    dense_trsv<T>(tp<T>(h->A), (int)g.n0, vt, xt, h->s_main);
     launch_scatter<T>(xi_out, xt, g.idx, g.N, h->s_main);
     if (int rc = finish(h, user)) return rc;
     if (*h->hinfo != 0) {
@@ -552,13 +557,14 @@ int op_grad_xi(ggp_graph* h, const T* vbar, T* xbar, hipStream_t user) {
     if (int rc = enter(h, user)) return rc;
     Graph& g = h->g;
     T *vbt = tp<T>(h->vbt), *vb = tp<T>(h->vb), *xg = tp<T>(h->xg);
-    launch_gather<T>(vbt, vbar, g.idx, g.N, h->s_main);
     if (int rc = fork(h)) return rc;
     dense_factor_async<T>(h, h->s_side);
+    launch_gather<T>(vbt, vbar, g.idx, g.N, h->s_main);
+    launch_sweep_prep<T>(g, nullptr, vb, h->s_main);
+    zero_tail<T>(h, xg, h->s_main);
     factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr,
                      nullptr);
-    zero_tail<T>(h, xg, h->s_main);
-    sweep_reverse<T>(h, vb, vbt, xg, h->s_main);
+    sweep_reverse<T>(h, vb, vbt, xg, h->s_main, true);
     if (int rc = join(h)) return rc;
     dense_trmv_t<T>(tp<T>(h->A), (int)g.n0, vb, xg, h->s_main);
     launch_scatter<T>(xbar, xg, g.idx, g.N, h->s_main);
@@ -618,18 +624,21 @@ int op_grad_vals(ggp_graph* h, int mode, int dkind, const T* in1, const T* in2, 
     launch_fill<int>(h->info, 0, 1, h->s_main);
     const T* pull_v = nullptr;
     if (mode == P_GENVALS) {  // generate_grad_vals: forward field, then the reverse sweep
-        launch_gather<T>(xt, in1, g.idx, g.N, h->s_main);
-        launch_gather<T>(vbt, in2, g.idx, g.N, h->s_main);
         if (int rc = fork(h)) return rc;
         dense_factor_async<T>(h, h->s_side);
-        dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_side);
-        factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr, nullptr);
-        if (int rc = join(h)) return rc;  // the sweeps need v[0:n0]
+        HC(hipEventRecord(h->ev_join, h->s_side));  // the factor is done
         // L^-1 needs only the factor: it runs beside both sweeps
         dense_inverse<T>(tp<T>(h->A), (int)g.n0, h->W, h->C, h->s_side);
+        launch_gather<T>(xt, in1, g.idx, g.N, h->s_main);
+        launch_gather<T>(vbt, in2, g.idx, g.N, h->s_main);
+        launch_sweep_prep<T>(g, v, vb, h->s_main);
         zero_tail<T>(h, v, h->s_main);
-        sweep_forward<T>(h, v, xt, g.n0, h->s_main);
-        sweep_reverse<T>(h, vb, vbt, nullptr, h->s_main);
+        factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr, nullptr);
+        // the sweeps need v[0:n0] = L xi[0:n0]: wait for the factor, not for the inverse
+        HC(hipStreamWaitEvent(h->s_main, h->ev_join, 0));
+        dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_main);
+        sweep_forward<T>(h, v, xt, g.n0, h->s_main, true);
+        sweep_reverse<T>(h, vb, vbt, nullptr, h->s_main, true);
         pull_v = v;
         if (int rc = fork(h)) return rc;
         dense_grad<T>(h, DG_GENERATE, h->s_side, true);
@@ -817,7 +826,7 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     if (const char* e = std::getenv("GGP_FACTOR_BLOCKS_PER_CU")) h->nblk_factor = (unsigned)(h->ncu * std::max(1, atoi(e)));
     else h->nblk_factor = (unsigned)(h->ncu * 4);
     if (const char* e = std::getenv("GGP_PULL_BLOCKS_PER_CU")) h->nblk_pull = (unsigned)(h->ncu * std::max(1, atoi(e)));
-    else h->nblk_pull = (unsigned)(h->ncu * 2);
+    else h->nblk_pull = (unsigned)(h->ncu * 6);  // the table + histogram LDS admits ~5 per CU
     // points per workgroup pass: kBlock (a lane per point) or kWideBlock/64 (a wavefront per point)
     const int64_t ppb = register_block_k(k) ? kBlock : kWideBlock / 64;
     if (!register_block_k(k)) {

@@ -903,27 +903,30 @@ static void dense_inverse64(const T* L, int n, double* W, double* S, hipStream_t
 
 // u = L^T vb (double), h/Q prefix pass: Q[a][j] = u[a] (sum_{j<=b<a} xi[b] W[b][j] + xi[a]W[a][j]/2)
 template <typename T>
-__global__ void k_ltv64(const T* __restrict__ L, int n, const T* __restrict__ vb,
-                        double* __restrict__ u) {
-    const int a = blockIdx.x * blockDim.x + threadIdx.x;
-    if (a >= n) return;
+__global__ void __launch_bounds__(64) k_ltv64(const T* __restrict__ L, int n,
+                                              const T* __restrict__ vb, double* __restrict__ u) {
+    // u[a] += sum over the 64 rows of this block's row chunk (rows >= a) of L[i][a] vb[i]
+    const int a = blockIdx.x * 64 + threadIdx.x;
+    const int i0 = blockIdx.y * 64;
+    if (a >= n || i0 + 63 < (int)(blockIdx.x * 64)) return;
     double s = 0.0;
-#pragma unroll 16
-    for (int i = a; i < n; ++i) s = __builtin_fma((double)L[(int64_t)i * n + a], (double)vb[i], s);
-    u[a] = s;
+    const int i1 = min(n, i0 + 64);
+#pragma unroll 8
+    for (int i = max(i0, a); i < i1; ++i) s = __builtin_fma((double)L[(int64_t)i * n + a], (double)vb[i], s);
+    atomicAdd(&u[a], s);
 }
 // Q[a][j] = u[a] (h_j(a) + xi[a] W[a][j] / 2), h_j(a) = sum_{b<a} xi[b] W[b][j] (W is lower
-// triangular, so rows above j add zeros). Workgroup = 32 columns x 8 row chunks: chunk sums,
+// triangular, so rows above j add zeros). Workgroup = 32 columns x 32 row chunks: chunk sums,
 // an exclusive prefix over the chunks in LDS, then the running sum within each chunk.
 template <typename T>
-__global__ void __launch_bounds__(256) k_qprefix(const double* __restrict__ W, int n,
-                                                 const T* __restrict__ xi,
-                                                 const double* __restrict__ u,
-                                                 double* __restrict__ Q) {
-    __shared__ double part[8][33];
+__global__ void __launch_bounds__(1024) k_qprefix(const double* __restrict__ W, int n,
+                                                  const T* __restrict__ xi,
+                                                  const double* __restrict__ u,
+                                                  double* __restrict__ Q) {
+    __shared__ double part[32][33];
     const int jl = threadIdx.x % 32, ck = threadIdx.x / 32;
     const int j = blockIdx.x * 32 + jl;
-    const int clen = (n + 7) / 8;
+    const int clen = (n + 31) / 32;
     const int a_lo = ck * clen, a_hi = min(n, a_lo + clen);
     double s = 0.0;
     if (j < n)
@@ -1038,8 +1041,9 @@ void dense_grad_generate(const Graph& g, const Table<T>& tb, const T* L, const T
                          double* hist_partial, int nw, bool inverse_ready, hipStream_t st) {
     const int n = (int)g.n0;
     if (!inverse_ready) dense_inverse64(L, n, W, C, st);
-    hipLaunchKernelGGL((k_ltv64<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, L, n, vb, u);
-    hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 32)), dim3(256), 0, st, W, n, xi, u, Q);
+    launch_fill<double>(u, 0.0, n, st);
+    hipLaunchKernelGGL((k_ltv64<T>), dim3(cdiv(n, 64), cdiv(n, 64)), dim3(64), 0, st, L, n, vb, u);
+    hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 32)), dim3(1024), 0, st, W, n, xi, u, Q);
     launch_gemm<double>({gemm_job(W, n, 1, Q, n, C, n, n, n, n, GK_FROM_I | GK_FROM_J, 1.0)}, st);
     launch_dense_scatter<T, DM_GENERATE>(g, tb, C, nullptr, hist_partial, nw, st);
 }

@@ -288,23 +288,51 @@ k_knn(const double* __restrict__ pts, const int8_t* __restrict__ split, int64_t 
 }
 
 // ---- 3. depths and the order by depth --------------------------------------------------------
-// One relaxation sweep of depth[n0+m] = 1 + max(0, depth[neighbours]); values only grow toward
-// the fixed point (the ordered pass of src/graph_build.jl:69-93), so sweeps may read values of
-// the same sweep.
-__global__ void k_depth_relax(const int32_t* __restrict__ nbr, int64_t n0, int64_t M, int k,
-                              int32_t* depth, int* changed) {
-    const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (m >= M) return;
-    int32_t mx = 0;
-    for (int j = 0; j < k; ++j) {
-        const int32_t d = __hip_atomic_load(&depth[nbr[m * k + j]], __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-        mx = d > mx ? d : mx;
-    }
-    const int32_t nd = mx + 1;
-    if (nd != __hip_atomic_load(&depth[n0 + m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-        __hip_atomic_store(&depth[n0 + m], nd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        atomicOr(changed, 1);
+// depth[n0+m] = 1 + max(0, depth[neighbours]) (compute_depths, src/graph_build.jl:69-93) in one
+// pass: refined points in position order (neighbours precede their point), 256 per chunk,
+// chunks taken by ticket, so a chunk only waits for chunks already taken by running
+// workgroups. Depths start at -1 (pending) and are published once. A wavefront retries its
+// lanes whose inputs are still pending, so no lane ever waits for a lane of its own
+// wavefront; later wavefronts only wait for earlier ones. Bounded: past the limit the
+// wavefront sets *err and stops.
+constexpr int kDepthSpinLimit = 1 << 22;
+__global__ void __launch_bounds__(kGbBlock)
+k_depth_flow(const int32_t* __restrict__ nbr, int64_t n0, int64_t M, int k, int32_t* depth,
+             int* ticket, int* err) {
+    __shared__ int s_c;
+    const int64_t nchunks = (M + kGbBlock - 1) / kGbBlock;
+    for (;;) {
+        __syncthreads();
+        if (threadIdx.x == 0) s_c = atomicAdd(ticket, 1);
+        __syncthreads();
+        const int c = __builtin_amdgcn_readfirstlane(s_c);
+        if (c >= nchunks) break;
+        const int64_t m = (int64_t)c * kGbBlock + threadIdx.x;
+        bool done = m >= M;
+        for (int spins = 0;; ++spins) {
+            if (!done) {
+                int32_t mx = 0;
+                bool ready = true;
+                for (int j = 0; j < k; ++j) {
+                    const int32_t d = __hip_atomic_load(&depth[nbr[m * k + j]], __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+                    ready = ready && d >= 0;
+                    mx = d > mx ? d : mx;
+                }
+                if (ready) {
+                    __hip_atomic_store(&depth[n0 + m], mx + 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    done = true;
+                }
+            }
+            if (__all(done)) break;
+            if (spins > kDepthSpinLimit) {
+                if (!done) atomicOr(err, 1);
+                break;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent");
+            __builtin_amdgcn_s_sleep(1);
+        }
     }
 }
 
@@ -509,24 +537,22 @@ int build(const double* points, int64_t N, int64_t n0, int k, int lattice_bits, 
 
     // 3. depths, then the stable order by depth
     GB_ALLOC(depth, int32_t, N);
-    GB_ALLOC(flag, int, 1);
-    int* hflag = nullptr;
-    GB_HC(hipHostMalloc((void**)&hflag, sizeof(int)));
-    struct HostFree {
-        int* p;
-        ~HostFree() { (void)hipHostFree(p); }
-    } hf{hflag};
-    hipLaunchKernelGGL(k_fill_i32, dim3(nblocks(N)), dim3(kGbBlock), 0, st, depth, 0, N);
-    for (int64_t rounds = 0;; ++rounds) {
-        if (rounds > M + 1) return set_error(GGP_ERR_HIP, "graph build: depths did not settle");
-        hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(1), 0, st, (int32_t*)flag, 0, 1);
-        for (int r = 0; r < 4; ++r)
-            hipLaunchKernelGGL(k_depth_relax, dim3(nblocks(M)), dim3(kGbBlock), 0, st, nbr, n0, M,
-                               k, depth, flag);
-        GB_HC(hipMemcpyAsync(hflag, flag, sizeof(int), hipMemcpyDeviceToHost, st));
-        GB_HC(hipStreamSynchronize(st));
-        if (*hflag == 0) break;
+    GB_ALLOC(sync2, int, 2);  // ticket, error
+    hipLaunchKernelGGL(k_fill_i32, dim3(nblocks(N)), dim3(kGbBlock), 0, st, depth, -1, N);
+    hipLaunchKernelGGL(k_fill_i32, dim3(nblocks(n0)), dim3(kGbBlock), 0, st, depth, 0, n0);
+    hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(kGbBlock), 0, st, sync2, 0, 2);
+    {
+        int dev = 0, ncu = 256;
+        if (hipGetDevice(&dev) == hipSuccess)
+            (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+        const unsigned nwg = (unsigned)std::max<int64_t>(1, std::min<int64_t>(ncu, (M + kGbBlock - 1) / kGbBlock));
+        hipLaunchKernelGGL(k_depth_flow, dim3(nwg), dim3(kGbBlock), 0, st, nbr, n0, M, k, depth,
+                           sync2, sync2 + 1);
     }
+    int derr = 0;
+    GB_HC(hipMemcpyAsync(&derr, sync2 + 1, sizeof(int), hipMemcpyDeviceToHost, st));
+    GB_HC(hipStreamSynchronize(st));
+    if (derr) return set_error(GGP_ERR_HIP, "graph build: a depth wait ran past its bound");
     hipLaunchKernelGGL(k_iota, dim3(nblocks(N)), dim3(kGbBlock), 0, st, val_a, N, (int64_t)0);
     {
         size_t tb = tmp_bytes;

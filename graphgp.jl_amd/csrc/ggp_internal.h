@@ -44,7 +44,7 @@ struct Graph {
     int4* fwd_chunks = nullptr;
     int4* rev_chunks = nullptr;
     int n_fwd_chunks = 0, n_rev_chunks = 0;
-    int* sweep_ticket = nullptr;   // 1 int, zeroed before each sweep
+    int* sweep_ticket = nullptr;   // [forward, reverse], zeroed before each sweep
     int* sweep_err = nullptr;      // bit 2: a wait ran past its bound
     int sweep_wgs = 1024;          // workgroups of a sweep launch
 };
@@ -135,14 +135,18 @@ void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, c
                      hipStream_t st);
 // Whole sweeps, one launch each: the forward apply over every level (v[n0:end] is written) and
 // the reverse gather (vb and xg of every position in a level or the dense block).
+// prepared: launch_sweep_prep already ran for this sweep (else the sweep prepares itself).
 template <typename T>
 void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                      const T* sd, bool two_pass, hipStream_t st);
+                      const T* sd, bool two_pass, bool prepared, hipStream_t st);
 template <typename T>
 void launch_sumsq_half(const T* x, int64_t n, double* out, hipStream_t st);
 template <typename T>
 void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                      hipStream_t st);
+                      bool prepared, hipStream_t st);
+// Pending markers for the next forward (v) and/or reverse (vb) sweep, tickets zeroed.
+template <typename T>
+void launch_sweep_prep(const Graph& g, T* v, T* vb, hipStream_t st);
 // p[0:n] = the pending marker of the sweeps (a NaN no arithmetic produces).
 template <typename T>
 void launch_fill_pending(T* p, int64_t n, hipStream_t st);

@@ -163,12 +163,33 @@ void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, c
 #undef CALLP
 }
 
+// Pending markers over the swept range of v and/or vb, and both tickets zeroed: one launch an
+// op issues early, off its critical path, instead of one fill before each sweep.
+template <typename U>
+__global__ void k_sweep_prep(U* __restrict__ a, U* __restrict__ b, U mark, int64_t n,
+                             int* __restrict__ tickets) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 2 && blockIdx.x == 0) tickets[i] = 0;
+    if (i < n) {
+        if (a) a[i] = mark;
+        if (b) b[i] = mark;
+    }
+}
+template <typename T>
+void launch_sweep_prep(const Graph& g, T* v, T* vb, hipStream_t st) {
+    using U = typename num<T>::bits_t;
+    const int64_t n = std::max<int64_t>(g.offsets.back() - g.n0, 1);
+    hipLaunchKernelGGL((k_sweep_prep<U>), dim3(grid_for(n)), dim3(kBlock), 0, st,
+                       v ? reinterpret_cast<U*>(v + g.n0) : nullptr,
+                       vb ? reinterpret_cast<U*>(vb + g.n0) : nullptr, (U)Pending<T>::bits,
+                       g.offsets.back() - g.n0, g.sweep_ticket);
+}
+
 template <typename T>
 void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                      const T* sd, bool two_pass, hipStream_t st) {
+                      const T* sd, bool two_pass, bool prepared, hipStream_t st) {
     if (g.n_fwd_chunks == 0) return;
-    launch_fill<int>(g.sweep_ticket, 0, 1, st);
-    launch_fill_pending<T>(v + g.n0, g.offsets.back() - g.n0, st);
+    if (!prepared) launch_sweep_prep<T>(g, v, (T*)nullptr, st);
 #define CALLS(KK) Launch<T, KK>::sweep_fwd(g, v, xi, xi_off, mv, sd, two_pass, st)
     GGP_FOR_K(CALLS);
 #undef CALLS
@@ -176,10 +197,9 @@ void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T
 
 template <typename T>
 void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                      hipStream_t st) {
+                      bool prepared, hipStream_t st) {
     if (g.n_rev_chunks == 0) return;
-    launch_fill<int>(g.sweep_ticket, 0, 1, st);
-    launch_fill_pending<T>(vb + g.n0, g.offsets.back() - g.n0, st);
+    if (!prepared) launch_sweep_prep<T>(g, (T*)nullptr, vb, st);
 #define CALLR(KK) Launch<T, KK>::sweep_rev(g, vb, vbar, xg, mv, sd, st)
     GGP_FOR_K(CALLR);
 #undef CALLR
@@ -253,9 +273,10 @@ void launch_points_out(T* out, const double* dp, const double* dpd, int64_t N, i
     template void launch_pullback<T>(const Graph&, const Table<T>&, int, const T*, const T*,   \
                                      const T*, double*, double*, unsigned, hipStream_t);       \
     template void launch_sweep_fwd<T>(const Graph&, T*, const T*, int64_t, const T*, const T*, \
-                                      bool, hipStream_t);                                      \
+                                      bool, bool, hipStream_t);                                \
     template void launch_sweep_rev<T>(const Graph&, T*, const T*, T*, const T*, const T*,      \
-                                      hipStream_t);                                            \
+                                      bool, hipStream_t);                                      \
+    template void launch_sweep_prep<T>(const Graph&, T*, T*, hipStream_t);                     \
     template void launch_fill_pending<T>(T*, int64_t, hipStream_t);                            \
     template void launch_reduce_hist<T>(T*, const double*, int, int, const double*,            \
                                         hipStream_t);                                          \

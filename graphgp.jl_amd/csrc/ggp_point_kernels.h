@@ -552,7 +552,7 @@ void PointK<T, K>::sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const 
     const unsigned nwg = (unsigned)std::max(1, std::min(g.n_rev_chunks, g.sweep_wgs));
     hipLaunchKernelGGL((k_sweep_rev<T, K>), dim3(nwg), dim3(kBlock), 0, st, vb, vbar, xg, mv, sd,
                        g.rcnt, g.rev, g.M, g.n0, (int)g.K, g.rev_chunks, g.n_rev_chunks,
-                       g.sweep_ticket, g.sweep_err);
+                       g.sweep_ticket + 1, g.sweep_err);
 }
 
 }  // namespace ggp
