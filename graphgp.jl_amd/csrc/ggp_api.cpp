@@ -70,7 +70,7 @@ struct ggp_graph {
     double *dp = nullptr, *dpd = nullptr;  // d/dpoints accumulators, N x D and n0 x D (lazy)
     std::vector<void*> owned;
     // optional HIP-event timers around the main kernels (ggp_kernel_timers)
-    bool timing = false;
+    int timing = 0;  // bit t: timer kTimerNames[t] is on
     hipEvent_t tev[2 * 8] = {};
     bool tpending[8] = {};
     double tms[8] = {};
@@ -205,10 +205,10 @@ const char* const kTimerNames[TM_COUNT] = {"factor", "pullback", "sweep_fwd", "s
                                            "dense", "op"};
 
 inline void tstart(ggp_graph* h, int t, hipStream_t st) {
-    if (h->timing) (void)hipEventRecord(h->tev[2 * t], st);
+    if (h->timing >> t & 1) (void)hipEventRecord(h->tev[2 * t], st);
 }
 inline void tstop(ggp_graph* h, int t, hipStream_t st) {
-    if (h->timing) {
+    if (h->timing >> t & 1) {
         (void)hipEventRecord(h->tev[2 * t + 1], st);
         h->tpending[t] = true;
     }
@@ -1053,7 +1053,7 @@ int ggp_kernel_timers(ggp_graph* h, int32_t enable) {
     if (enable && !h->tev[0])
         for (int i = 0; i < 2 * TM_COUNT; ++i)
             if (hipEventCreate(&h->tev[i]) != hipSuccess) return fail(GGP_ERR_HIP, "hipEventCreate failed");
-    h->timing = enable != 0;
+    h->timing = enable & ((1 << TM_COUNT) - 1);
     for (int t = 0; t < TM_COUNT; ++t) { h->tms[t] = 0; h->tcnt[t] = 0; h->tpending[t] = false; }
     return 0;
 }

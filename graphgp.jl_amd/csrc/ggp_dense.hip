@@ -916,17 +916,17 @@ __global__ void __launch_bounds__(64) k_ltv64(const T* __restrict__ L, int n,
     atomicAdd(&u[a], s);
 }
 // Q[a][j] = u[a] (h_j(a) + xi[a] W[a][j] / 2), h_j(a) = sum_{b<a} xi[b] W[b][j] (W is lower
-// triangular, so rows above j add zeros). Workgroup = 32 columns x 32 row chunks: chunk sums,
+// triangular, so rows above j add zeros). Workgroup = 32 columns x 8 row chunks: chunk sums,
 // an exclusive prefix over the chunks in LDS, then the running sum within each chunk.
 template <typename T>
-__global__ void __launch_bounds__(1024) k_qprefix(const double* __restrict__ W, int n,
-                                                  const T* __restrict__ xi,
-                                                  const double* __restrict__ u,
-                                                  double* __restrict__ Q) {
-    __shared__ double part[32][33];
+__global__ void __launch_bounds__(256) k_qprefix(const double* __restrict__ W, int n,
+                                                 const T* __restrict__ xi,
+                                                 const double* __restrict__ u,
+                                                 double* __restrict__ Q) {
+    __shared__ double part[8][33];
     const int jl = threadIdx.x % 32, ck = threadIdx.x / 32;
     const int j = blockIdx.x * 32 + jl;
-    const int clen = (n + 31) / 32;
+    const int clen = (n + 7) / 8;
     const int a_lo = ck * clen, a_hi = min(n, a_lo + clen);
     double s = 0.0;
     if (j < n)
@@ -1043,7 +1043,7 @@ void dense_grad_generate(const Graph& g, const Table<T>& tb, const T* L, const T
     if (!inverse_ready) dense_inverse64(L, n, W, C, st);
     launch_fill<double>(u, 0.0, n, st);
     hipLaunchKernelGGL((k_ltv64<T>), dim3(cdiv(n, 64), cdiv(n, 64)), dim3(64), 0, st, L, n, vb, u);
-    hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 32)), dim3(1024), 0, st, W, n, xi, u, Q);
+    hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 32)), dim3(256), 0, st, W, n, xi, u, Q);
     launch_gemm<double>({gemm_job(W, n, 1, Q, n, C, n, n, n, n, GK_FROM_I | GK_FROM_J, 1.0)}, st);
     launch_dense_scatter<T, DM_GENERATE>(g, tb, C, nullptr, hist_partial, nw, st);
 }

@@ -185,9 +185,11 @@ int ggp_build_graph_device(const double* points, int64_t N, int32_t D, int64_t n
 
 /* ---- measurement ------------------------------------------------------------------------- */
 /* No counterpart in the reference (its benchmarks time whole calls, bench/compare/run_julia.jl:50-58).
- * When enabled, each op brackets its main kernels with HIP events on the stream they run on;
- * ggp_kernel_timer_read returns the summed milliseconds and the number of timed launches for
- * "factor", "pullback", "sweep_fwd", "sweep_rev", "dense" or "op" (whole op). Enabling resets. */
+ * `enable` is a bit mask over "factor" (1), "pullback" (2), "sweep_fwd" (4), "sweep_rev" (8),
+ * "dense" (16) and "op" (32, the whole op); 0 turns timing off, 63 times everything. Each
+ * enabled timer brackets its kernels with HIP events on the stream they run on (every event
+ * pair adds a few microseconds to the op); ggp_kernel_timer_read returns the summed
+ * milliseconds and the number of timed launches for one name. Enabling resets the sums. */
 int ggp_kernel_timers(ggp_graph* h, int32_t enable);
 int ggp_kernel_timer_read(const ggp_graph* h, const char* name, double* total_ms, int64_t* count);
 
