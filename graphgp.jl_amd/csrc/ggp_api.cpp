@@ -164,7 +164,20 @@ int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
         while (lo + 1 <= nb - 2 && bins[lo + 1] <= cm) ++lo;
         acc[(size_t)c + 1] = (uint16_t)std::min<int64_t>(lo, nb - 2);
     }
+    // Most forward steps the search takes from acc[cell] for any r < bins[nb-1] in the cell
+    // (the kernels use one unconditional step when this is <= 1).
+    int steps = 0;
+    const U top_all = Bits<T>::of(bins[nb - 1]) - 1;
+    for (int c = 0; c < ucells; ++c) {
+        const U top = std::min<U>(base + (((U)c + 1) << shift) - 1, top_all);
+        const T vmax = Bits<T>::from(top);
+        int64_t hi = acc[(size_t)c + 1];
+        const int64_t lo0 = hi;
+        while (hi + 1 <= nb - 2 && bins[hi + 1] <= vmax) ++hi;
+        steps = std::max<int>(steps, (int)(hi - lo0));
+    }
     TabParams<T> P{};
+    P.steps = steps;
     P.b0 = bins[0];
     P.b1 = bins[1];
     P.bl = bins[nb - 1];
@@ -1055,6 +1068,23 @@ int ggp_kernel_timers(ggp_graph* h, int32_t enable) {
             if (hipEventCreate(&h->tev[i]) != hipSuccess) return fail(GGP_ERR_HIP, "hipEventCreate failed");
     h->timing = enable & ((1 << TM_COUNT) - 1);
     for (int t = 0; t < TM_COUNT; ++t) { h->tms[t] = 0; h->tcnt[t] = 0; h->tpending[t] = false; }
+    return 0;
+}
+
+int ggp_selftest_sqrt_f32(uint32_t first_bits, uint32_t count, uint64_t* mismatches) {
+    if (!mismatches) return fail(GGP_ERR_ARG, "null argument");
+    unsigned long long* d = nullptr;
+    HC(hipMalloc((void**)&d, sizeof(*d)));
+    hipError_t e = hipMemset(d, 0, sizeof(*d));
+    if (e == hipSuccess && count) {
+        ggp::launch_sqrt_check(first_bits, count, d, nullptr);
+        e = hipGetLastError();
+    }
+    unsigned long long hbad = 0;
+    if (e == hipSuccess) e = hipMemcpy(&hbad, d, sizeof(hbad), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return fail(GGP_ERR_HIP, std::string("sqrt self-test: ") + hipGetErrorString(e));
+    *mismatches = hbad;
     return 0;
 }
 

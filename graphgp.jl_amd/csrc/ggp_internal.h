@@ -169,6 +169,9 @@ template <typename T>
 void launch_points_out(T* out, const double* dp, const double* dpd, int64_t N, int D,
                        int64_t n_dense, const int32_t* map, hipStream_t st);
 
+// Self-check of the lattice square root (sqrt_rn_f32) over bit patterns [b0, b0 + count).
+void launch_sqrt_check(uint32_t b0, uint32_t count, unsigned long long* bad, hipStream_t st);
+
 // Dense first layer (ggp_dense.hip). Matrices are n x n row-major; L lower.
 template <typename T>
 void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStream_t st);

@@ -267,6 +267,22 @@ void launch_points_out(T* out, const double* dp, const double* dpd, int64_t N, i
                            dpd, N, D, n_dense, map);
 }
 
+// Self-check of sqrt_rn_f32 against the correctly rounded sqrtf over `count` consecutive bit
+// patterns from b0; *bad receives the number of differing results.
+__global__ void __launch_bounds__(256) k_sqrt_check(uint32_t b0, uint32_t count,
+                                                    unsigned long long* __restrict__ bad) {
+    const uint32_t stride = gridDim.x * blockDim.x;
+    unsigned long long nbad = 0;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+        const float x = __uint_as_float(b0 + i);
+        nbad += __float_as_uint(sqrt_rn_f32(x)) != __float_as_uint(__builtin_sqrtf(x));
+    }
+    if (nbad) atomicAdd(bad, nbad);
+}
+void launch_sqrt_check(uint32_t b0, uint32_t count, unsigned long long* bad, hipStream_t st) {
+    hipLaunchKernelGGL(k_sqrt_check, dim3(4096), dim3(256), 0, st, b0, count, bad);
+}
+
 #define GGP_INST(T)                                                                            \
     template void launch_factor<T>(const Graph&, const Table<T>&, int, T*, T*, T*, double*,    \
                                    const T*, T*, unsigned, hipStream_t);                       \

@@ -88,46 +88,73 @@ template <typename T> struct TabParams {
     int shift;                     // cell width in ulps = 2^shift
     int ucells;                    // number of cells U; acc has U+1 entries
     int nb;                        // number of bins
+    int steps;                     // most forward steps any r in [b0, bl) needs from acc[cell]
 };
 
-template <typename T>
+// ONE: the table has steps <= 1 (every cell holds at most one bin edge, as on log-spaced tables),
+// so the search is one unconditional step and the lookup has no branch: the out-of-range cases
+// are selected afterwards, the lookup itself running on an in-range stand-in. The kernels choose
+// ONE once per launch from P.steps; both forms return the same lo.
+template <typename T, bool ONE>
 __device__ inline int seg_index(T r, const TabEnt<T>* __restrict__ tab,
                                 const uint16_t* __restrict__ acc, const TabParams<T>& P) {
     using S = typename num<T>::sbits_t;
     S d = (S)(num<T>::bits(r) - P.base);
     int cell = d < 0 ? 0 : (int)min((S)(d >> P.shift) + 1, (S)P.ucells);
     int lo = acc[cell];
-    while (r >= tab[lo].x1) ++lo;  // bounded: bins[nb-1] > r here
+    if (ONE) lo += r >= tab[lo].x1 ? 1 : 0;
+    else while (r >= tab[lo].x1) ++lo;  // bounded: bins[nb-1] > r here
     return lo;
 }
 
 // cov_lookup (src/interp.jl:10-34).
-template <typename T>
+template <typename T, bool ONE = false>
 __device__ inline T cov_lookup(T r, const TabEnt<T>* __restrict__ tab,
                                const uint16_t* __restrict__ acc, const TabParams<T>& P) {
+    if (ONE) {
+        const T rr = r < P.bl ? r : P.b0;
+        const TabEnt<T> e = tab[seg_index<T, true>(rr, tab, acc, P)];
+        const T v = num<T>::fma(e.slope, rr - e.x0, e.y0);
+        return r <= P.b0 ? P.v0 : (r >= P.bl ? P.vl : v);
+    }
     if (r <= P.b0) return P.v0;
     if (r >= P.bl) return P.vl;
-    const TabEnt<T> e = tab[seg_index(r, tab, acc, P)];
+    const TabEnt<T> e = tab[seg_index<T, false>(r, tab, acc, P)];
     return num<T>::fma(e.slope, r - e.x0, e.y0);  // @fastmath y0 + slope*(r - x0)
 }
 
 // cov_lookup_dr (src/interp.jl:43-60): d cov / d r, the bracketing segment's slope; 0 at or
 // beyond either end of the table.
-template <typename T>
+template <typename T, bool ONE = false>
 __device__ inline T cov_slope(T r, const TabEnt<T>* __restrict__ tab,
                               const uint16_t* __restrict__ acc, const TabParams<T>& P) {
+    if (ONE) {
+        const T rr = r < P.bl ? r : P.b0;
+        const T sl = tab[seg_index<T, true>(rr, tab, acc, P)].slope;
+        return (r <= P.b0 || r >= P.bl) ? T(0) : sl;
+    }
     if (r <= P.b0 || r >= P.bl) return T(0);
-    return tab[seg_index(r, tab, acc, P)].slope;
+    return tab[seg_index<T, false>(r, tab, acc, P)].slope;
 }
 
 // cov_lookup_weights (src/interp.jl:62-83): value = wlo*vals[lo] + whi*vals[lo+1].
-template <typename T>
+template <typename T, bool ONE = false>
 __device__ inline int cov_weights(T r, const TabEnt<T>* __restrict__ tab,
                                   const uint16_t* __restrict__ acc, const TabParams<T>& P,
                                   T& wlo, T& whi) {
+    if (ONE) {
+        const T rr = r < P.bl ? r : P.b0;
+        const int lo = seg_index<T, true>(rr, tab, acc, P);
+        const TabEnt<T> e = tab[lo];
+        const T t = (rr - e.x0) / (e.x1 - e.x0);
+        const bool below = r <= P.b0, above = r >= P.bl;
+        wlo = below ? T(1) : (above ? T(0) : T(1) - t);
+        whi = below ? T(0) : (above ? T(1) : t);
+        return below ? 0 : (above ? P.nb - 2 : lo);
+    }
     if (r <= P.b0) { wlo = T(1); whi = T(0); return 0; }
     if (r >= P.bl) { wlo = T(0); whi = T(1); return P.nb - 2; }
-    const int lo = seg_index(r, tab, acc, P);
+    const int lo = seg_index<T, false>(r, tab, acc, P);
     const TabEnt<T> e = tab[lo];
     const T t = (r - e.x0) / (e.x1 - e.x0);
     wlo = T(1) - t;
@@ -149,16 +176,35 @@ __device__ inline double sqdist(const uint32_t (&a)[D], const uint32_t (&b)[D]) 
     return s;
 }
 
-// r = sqrt(T(sq)) * scale (src/linalg.jl:24; src/kernels_adjoint.jl:34).
+// Correctly rounded square root of x = 0 or x >= 1e-30 (f32), without the range scaling and
+// special-value handling of the general sequence. v_sqrt_f32 is within 1 ulp of sqrt(x), so the
+// correctly rounded result is s or one of its neighbours s-, s+; the exact residuals x - s-*s and
+// x - s+*s (one fma each) decide which: no float lies strictly between s-*s and (s-1/2ulp)^2,
+// nor between s*s+ and (s+1/2ulp)^2. Checked against sqrtf bit for bit over every float in
+// [1e-30, 2^64] and 0 (selftest_sqrt).
+__device__ inline float sqrt_rn_f32(float x) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const float sdn = __uint_as_float(__float_as_uint(s) - 1u);
+    const float sup = __uint_as_float(__float_as_uint(s) + 1u);
+    const float rdn = __builtin_fmaf(-sdn, s, x);
+    const float rup = __builtin_fmaf(-sup, s, x);
+    const float y = rdn <= 0.f ? sdn : s;
+    return rup > 0.f ? sup : y;
+}
+template <typename T> __device__ inline T sqrt_lattice(T x) { return num<T>::sqrt(x); }
+template <> __device__ inline float sqrt_lattice<float>(float x) { return sqrt_rn_f32(x); }
+
+// r = sqrt(T(sq)) * scale (src/linalg.jl:24; src/kernels_adjoint.jl:34). T(sq) is 0 or an
+// integer >= 1, inside the fast square root's range.
 template <typename T>
 __device__ inline T radius(double sq, T scale) {
-    return num<T>::sqrt((T)sq) * scale;
+    return sqrt_lattice<T>((T)sq) * scale;
 }
 
 // One pair's contribution to d/dpoints (src/kernels_adjoint.jl:223-252): the off-diagonal
 // cotangent g of the pair (a, b) through k'(r) dr/dx; c[d] is what point a gains and point b
 // loses. Returns false (c untouched) for coincident points and radii outside the table.
-template <typename T, int D>
+template <typename T, int D, bool ONE = false>
 __device__ inline bool pair_pts(const uint32_t (&ca)[D], const uint32_t (&cb)[D], T g, T scale,
                                 const TabEnt<T>* __restrict__ tab,
                                 const uint16_t* __restrict__ acc, const TabParams<T>& P,
@@ -166,7 +212,7 @@ __device__ inline bool pair_pts(const uint32_t (&ca)[D], const uint32_t (&cb)[D]
     const double sq = sqdist<D>(ca, cb);
     if (sq == 0.0) return false;
     const T r = radius<T>(sq, scale);
-    const T dcov = cov_slope(r, tab, acc, P);
+    const T dcov = cov_slope<T, ONE>(r, tab, acc, P);
     if (dcov == T(0)) return false;
     const T f = g * dcov / r;
 #pragma unroll
@@ -258,6 +304,7 @@ struct Block {
     }
 
     // assemble_cov! (src/linalg.jl:15-29).
+    template <bool ONE = false>
     __device__ inline void assemble(T scale, const TabEnt<T>* __restrict__ tab,
                                     const uint16_t* __restrict__ acc, const TabParams<T>& P) {
 #pragma unroll
@@ -265,7 +312,8 @@ struct Block {
             A[tri(a, a)] = P.v0;  // cov_lookup(0) = vals[1] since bins[1] = 0 <= 0
 #pragma unroll
             for (int b = 0; b < a; ++b)
-                A[tri(a, b)] = cov_lookup(radius<T>(sqdist<D>(jc[a], jc[b]), scale), tab, acc, P);
+                A[tri(a, b)] = cov_lookup<T, ONE>(radius<T>(sqdist<D>(jc[a], jc[b]), scale), tab,
+                                                  acc, P);
         }
     }
 

@@ -49,26 +49,16 @@ __device__ inline double block_sum(double v, double* s_red) {
 }
 
 // ---- factor pass ----------------------------------------------------------------------------
-// ANISO: the covariance comes from the anisotropic grid (src/aniso.jl) instead of (bins, vals).
-template <typename T, int K, int D, int MODE, bool ANISO>
-__global__ void __launch_bounds__(kBlock)
-k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, int64_t M,
-         int64_t n0, T scale, const TabEnt<T>* __restrict__ g_tab,
-         const uint16_t* __restrict__ g_acc, const TabParams<T>* __restrict__ Pp, T* __restrict__ mv,
-         T* __restrict__ sd, T* __restrict__ terms, double* __restrict__ partial,
-         const T* __restrict__ values, T* __restrict__ xi_out, AnisoArgs<T> an) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ double s_red[kBlock / 64];
-    TabParams<T> P{};
-    TabEnt<T>* s_tab = nullptr;
-    uint16_t* s_acc = nullptr;
-    if (!ANISO) {
-        P = *Pp;
-        s_tab = reinterpret_cast<TabEnt<T>*>(smem);
-        s_acc = reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
-        stage_table(s_tab, s_acc, g_tab, g_acc, P);
-    }
-
+// The grid-stride loop of k_factor over the refined points; returns this lane's sum of the
+// logdet terms. ONE: the single-step table search (P.steps <= 1).
+template <typename T, int K, int D, int MODE, bool ANISO, bool ONE>
+__device__ inline double factor_points(const uint32_t* __restrict__ coords,
+                                       const int32_t* __restrict__ nbr, int64_t M, int64_t n0,
+                                       T scale, const TabEnt<T>* s_tab, const uint16_t* s_acc,
+                                       const TabParams<T>& P, T* __restrict__ mv,
+                                       T* __restrict__ sd, T* __restrict__ terms,
+                                       const T* __restrict__ values, T* __restrict__ xi_out,
+                                       const AnisoArgs<T>& an) {
     double lsum = 0.0;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; m < M; m += stride) {
@@ -76,7 +66,7 @@ k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, i
         int32_t nb[K];
         blk.gather(coords, nbr, M, m, n0, nb);
         if (ANISO) blk.assemble_aniso(scale, an);
-        else blk.assemble(scale, s_tab, s_acc, P);
+        else blk.template assemble<ONE>(scale, s_tab, s_acc, P);
         blk.cholesky();
         const T s = blk.stddev();
         if (MODE & F_TERMS) {
@@ -100,11 +90,42 @@ k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, i
             }
         }
     }
+    return lsum;
+}
+
+// ANISO: the covariance comes from the anisotropic grid (src/aniso.jl) instead of (bins, vals).
+template <typename T, int K, int D, int MODE, bool ANISO>
+__global__ void __launch_bounds__(kBlock)
+k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, int64_t M,
+         int64_t n0, T scale, const TabEnt<T>* __restrict__ g_tab,
+         const uint16_t* __restrict__ g_acc, const TabParams<T>* __restrict__ Pp, T* __restrict__ mv,
+         T* __restrict__ sd, T* __restrict__ terms, double* __restrict__ partial,
+         const T* __restrict__ values, T* __restrict__ xi_out, AnisoArgs<T> an) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ double s_red[kBlock / 64];
+    TabParams<T> P{};
+    TabEnt<T>* s_tab = nullptr;
+    uint16_t* s_acc = nullptr;
+    if (!ANISO) {
+        P = *Pp;
+        s_tab = reinterpret_cast<TabEnt<T>*>(smem);
+        s_acc = reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
+        stage_table(s_tab, s_acc, g_tab, g_acc, P);
+    }
+
+    double lsum = 0.0;
+    if (ANISO || P.steps <= 1)
+        lsum = factor_points<T, K, D, MODE, ANISO, true>(coords, nbr, M, n0, scale, s_tab, s_acc,
+                                                         P, mv, sd, terms, values, xi_out, an);
+    else
+        lsum = factor_points<T, K, D, MODE, ANISO, false>(coords, nbr, M, n0, scale, s_tab, s_acc,
+                                                          P, mv, sd, terms, values, xi_out, an);
     if (MODE & F_TERMS) {
         const double t = block_sum(lsum, s_red);
         if (threadIdx.x == 0) partial[blockIdx.x] = t;
     }
 }
+
 
 // ---- level sweeps: one persistent launch per sweep ----------------------------------------
 // Every value a sweep produces starts as a pending marker (a NaN no arithmetic produces) and is
@@ -305,7 +326,7 @@ k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
 
 // ---- adjoint pullback -----------------------------------------------------------------------
 // Histogram scatter of one point's Abar through the lookup weights (src/kernels_adjoint.jl:47-74).
-template <typename T, int K, int D>
+template <typename T, int K, int D, bool ONE>
 __device__ inline void scatter_hist(double* hist, const Block<T, K, D>& blk,
                                     const T (&Abar)[(K + 1) * (K + 2) / 2], T scale,
                                     const TabEnt<T>* tab, const uint16_t* acc,
@@ -321,7 +342,7 @@ __device__ inline void scatter_hist(double* hist, const Block<T, K, D>& blk,
         for (int b = 0; b < a; ++b) {
             const T r = radius<T>(sqdist<D>(blk.jc[a], blk.jc[b]), scale);
             T wlo, whi;
-            const int lo = cov_weights(r, tab, acc, P, wlo, whi);
+            const int lo = cov_weights<T, ONE>(r, tab, acc, P, wlo, whi);
             const T g = Abar[tri(a, b)];
             atomicAdd(&hist[lo], (double)(g * wlo));
             atomicAdd(&hist[lo + 1], (double)(g * whi));
@@ -331,7 +352,7 @@ __device__ inline void scatter_hist(double* hist, const Block<T, K, D>& blk,
 // d/dpoints scatter of one point's Abar (src/kernels_adjoint.jl:223-252): each pair's term is
 // summed per block row in double, then one f64 atomic add per row and coordinate into dp
 // (N x D, tree order).
-template <typename T, int K, int D>
+template <typename T, int K, int D, bool ONE>
 __device__ inline void scatter_pts(double* dp, const Block<T, K, D>& blk, const int32_t (&nb)[K],
                                    int64_t m, int64_t n0,
                                    const T (&Abar)[(K + 1) * (K + 2) / 2], T scale,
@@ -348,7 +369,7 @@ __device__ inline void scatter_pts(double* dp, const Block<T, K, D>& blk, const 
 #pragma unroll
         for (int b = 0; b < a; ++b) {
             T c[D];
-            if (pair_pts<T, D>(blk.jc[a], blk.jc[b], Abar[tri(a, b)], scale, tab, acc, P, c)) {
+            if (pair_pts<T, D, ONE>(blk.jc[a], blk.jc[b], Abar[tri(a, b)], scale, tab, acc, P, c)) {
 #pragma unroll
                 for (int d = 0; d < D; ++d) {
                     g[a][d] += (double)c[d];
@@ -364,29 +385,17 @@ __device__ inline void scatter_pts(double* dp, const Block<T, K, D>& blk, const 
     }
 }
 
-// MODE: P_LOGDET / P_INVLOSS / P_GENVALS seeds the factor cotangents; with P_PTS added, Abar goes
-// to the point positions (hist_partial is then dp, N x D) instead of the table histogram.
-template <typename T, int K, int D, int MODE>
-__global__ void __launch_bounds__(kBlock)
-k_pullback(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, int64_t M,
-           int64_t n0, T scale, const TabEnt<T>* __restrict__ g_tab,
-           const uint16_t* __restrict__ g_acc, const TabParams<T>* __restrict__ Pp,
-           const T* __restrict__ v,     // INVLOSS: values (tree order); GENVALS: forward field
-           const T* __restrict__ xi,    // GENVALS: xi (tree order)
-           const T* __restrict__ vb,    // GENVALS: field cotangent after the reverse sweep
-           double* __restrict__ hist_partial, double* __restrict__ scalar_partial) {
+// The grid-stride loop of k_pullback over the refined points; returns this lane's sum of the
+// scalar terms. ONE: the single-step table search (P.steps <= 1).
+template <typename T, int K, int D, int MODE, bool ONE>
+__device__ inline double pullback_points(const uint32_t* __restrict__ coords,
+                                         const int32_t* __restrict__ nbr, int64_t M, int64_t n0,
+                                         T scale, const TabEnt<T>* s_tab, const uint16_t* s_acc,
+                                         const TabParams<T>& P, const T* __restrict__ v,
+                                         const T* __restrict__ xi, const T* __restrict__ vb,
+                                         double* __restrict__ hist_partial, double* s_hist) {
     constexpr int SEED = MODE & 3;
     constexpr bool PTS = (MODE & P_PTS) != 0;
-    const TabParams<T> P = *Pp;
-    extern __shared__ __align__(16) unsigned char smem[];
-    TabEnt<T>* s_tab = reinterpret_cast<TabEnt<T>*>(smem);
-    uint16_t* s_acc = reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
-    double* s_hist = reinterpret_cast<double*>(smem + tab_bytes<T>(P.nb, P.ucells));
-    __shared__ double s_red[kBlock / 64];
-    if (!PTS)
-        for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
-    stage_table(s_tab, s_acc, g_tab, g_acc, P);
-
     constexpr int N = K + 1;
     constexpr int NT = N * (N + 1) / 2;
     double ssum = 0.0;
@@ -395,7 +404,7 @@ k_pullback(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
         Block<T, K, D> blk;
         int32_t nb[K];
         blk.gather(coords, nbr, M, m, n0, nb);
-        blk.assemble(scale, s_tab, s_acc, P);
+        blk.template assemble<ONE>(scale, s_tab, s_acc, P);
         blk.cholesky();
         const T s = blk.stddev();
         T Lbar[NT], Abar[NT];
@@ -450,10 +459,42 @@ k_pullback(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
         }
         chol_pullback<T, N>(Abar, Lbar, blk.A);
         if (PTS)
-            scatter_pts<T, K, D>(hist_partial, blk, nb, m, n0, Abar, scale, s_tab, s_acc, P);
+            scatter_pts<T, K, D, ONE>(hist_partial, blk, nb, m, n0, Abar, scale, s_tab, s_acc, P);
         else
-            scatter_hist<T, K, D>(s_hist, blk, Abar, scale, s_tab, s_acc, P);
+            scatter_hist<T, K, D, ONE>(s_hist, blk, Abar, scale, s_tab, s_acc, P);
     }
+    return ssum;
+}
+
+// MODE: P_LOGDET / P_INVLOSS / P_GENVALS seeds the factor cotangents; with P_PTS added, Abar goes
+// to the point positions (hist_partial is then dp, N x D) instead of the table histogram.
+template <typename T, int K, int D, int MODE>
+__global__ void __launch_bounds__(kBlock)
+k_pullback(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, int64_t M,
+           int64_t n0, T scale, const TabEnt<T>* __restrict__ g_tab,
+           const uint16_t* __restrict__ g_acc, const TabParams<T>* __restrict__ Pp,
+           const T* __restrict__ v,     // INVLOSS: values (tree order); GENVALS: forward field
+           const T* __restrict__ xi,    // GENVALS: xi (tree order)
+           const T* __restrict__ vb,    // GENVALS: field cotangent after the reverse sweep
+           double* __restrict__ hist_partial, double* __restrict__ scalar_partial) {
+    constexpr bool PTS = (MODE & P_PTS) != 0;
+    const TabParams<T> P = *Pp;
+    extern __shared__ __align__(16) unsigned char smem[];
+    TabEnt<T>* s_tab = reinterpret_cast<TabEnt<T>*>(smem);
+    uint16_t* s_acc = reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
+    double* s_hist = reinterpret_cast<double*>(smem + tab_bytes<T>(P.nb, P.ucells));
+    __shared__ double s_red[kBlock / 64];
+    if (!PTS)
+        for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
+    stage_table(s_tab, s_acc, g_tab, g_acc, P);
+
+    double ssum;
+    if (P.steps <= 1)
+        ssum = pullback_points<T, K, D, MODE, true>(coords, nbr, M, n0, scale, s_tab, s_acc, P, v,
+                                                    xi, vb, hist_partial, s_hist);
+    else
+        ssum = pullback_points<T, K, D, MODE, false>(coords, nbr, M, n0, scale, s_tab, s_acc, P, v,
+                                                     xi, vb, hist_partial, s_hist);
     __syncthreads();
     if (!PTS) {
         double* out = hist_partial + (size_t)blockIdx.x * P.nb;

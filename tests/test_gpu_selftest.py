@@ -1,0 +1,22 @@
+"""Self-check of the f32 square root the per-point kernels use for pair radii: it must equal the
+correctly rounded sqrtf bit for bit over every float the kernels can pass it (0 and the integers
+up to 2^46, the squared lattice distances) and beyond, on the device itself."""
+import ctypes as C
+import struct
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(x):
+    return struct.unpack("<I", struct.pack("<f", x))[0]
+
+
+@pytest.mark.parametrize("lo,hi", [(0.0, 0.0), (1.0, 2.0 ** 64), (1e-30, 1.0)])
+def test_lattice_sqrt_is_correctly_rounded(gpu, lo, hi):
+    from graphgp_hip import _native as nat
+    b0, b1 = _bits(lo), _bits(hi)
+    bad = C.c_uint64(0)
+    nat.call("ggp_selftest_sqrt_f32", b0, b1 - b0 + 1, C.byref(bad))
+    assert bad.value == 0
