@@ -112,10 +112,13 @@ template <typename T, bool ONE = false>
 __device__ inline T cov_lookup(T r, const TabEnt<T>* __restrict__ tab,
                                const uint16_t* __restrict__ acc, const TabParams<T>& P) {
     if (ONE) {
-        const T rr = r < P.bl ? r : P.b0;
+        const T b0 = P.b0, bl = P.bl, v0 = P.v0, vl = P.vl;
+        const bool below = r <= b0, above = r >= bl;
+        const T rr = above ? b0 : r;
         const TabEnt<T> e = tab[seg_index<T, true>(rr, tab, acc, P)];
-        const T v = num<T>::fma(e.slope, rr - e.x0, e.y0);
-        return r <= P.b0 ? P.v0 : (r >= P.bl ? P.vl : v);
+        T v = num<T>::fma(e.slope, rr - e.x0, e.y0);
+        v = above ? vl : v;
+        return below ? v0 : v;
     }
     if (r <= P.b0) return P.v0;
     if (r >= P.bl) return P.vl;
@@ -129,9 +132,11 @@ template <typename T, bool ONE = false>
 __device__ inline T cov_slope(T r, const TabEnt<T>* __restrict__ tab,
                               const uint16_t* __restrict__ acc, const TabParams<T>& P) {
     if (ONE) {
-        const T rr = r < P.bl ? r : P.b0;
+        const T b0 = P.b0, bl = P.bl;
+        const bool out = r <= b0 || r >= bl;
+        const T rr = r >= bl ? b0 : r;
         const T sl = tab[seg_index<T, true>(rr, tab, acc, P)].slope;
-        return (r <= P.b0 || r >= P.bl) ? T(0) : sl;
+        return out ? T(0) : sl;
     }
     if (r <= P.b0 || r >= P.bl) return T(0);
     return tab[seg_index<T, false>(r, tab, acc, P)].slope;
@@ -143,14 +148,20 @@ __device__ inline int cov_weights(T r, const TabEnt<T>* __restrict__ tab,
                                   const uint16_t* __restrict__ acc, const TabParams<T>& P,
                                   T& wlo, T& whi) {
     if (ONE) {
-        const T rr = r < P.bl ? r : P.b0;
+        const T b0 = P.b0, bl = P.bl;
+        const int last = P.nb - 2;
+        const bool below = r <= b0, above = r >= bl;
+        const T rr = above ? b0 : r;
         const int lo = seg_index<T, true>(rr, tab, acc, P);
         const TabEnt<T> e = tab[lo];
         const T t = (rr - e.x0) / (e.x1 - e.x0);
-        const bool below = r <= P.b0, above = r >= P.bl;
-        wlo = below ? T(1) : (above ? T(0) : T(1) - t);
-        whi = below ? T(0) : (above ? T(1) : t);
-        return below ? 0 : (above ? P.nb - 2 : lo);
+        T wl = T(1) - t, wh = t;
+        wl = above ? T(0) : wl;
+        wh = above ? T(1) : wh;
+        wlo = below ? T(1) : wl;
+        whi = below ? T(0) : wh;
+        const int l2 = above ? last : lo;
+        return below ? 0 : l2;
     }
     if (r <= P.b0) { wlo = T(1); whi = T(0); return 0; }
     if (r >= P.bl) { wlo = T(0); whi = T(1); return P.nb - 2; }
@@ -303,17 +314,47 @@ struct Block {
         for (int d = 0; d < D; ++d) jc[K][d] = c[d];
     }
 
-    // assemble_cov! (src/linalg.jl:15-29).
-    template <bool ONE = false>
+    // assemble_cov! (src/linalg.jl:15-29). With ROWS (single-step tables only) the lookups of
+    // one row run phase by phase (radii, cell reads, step reads, entry reads), so their LDS round
+    // trips overlap, at the cost of registers; each entry is the value cov_lookup returns.
+    template <bool ONE = false, bool ROWS = false>
     __device__ inline void assemble(T scale, const TabEnt<T>* __restrict__ tab,
                                     const uint16_t* __restrict__ acc, const TabParams<T>& P) {
+        if (!(ONE && ROWS)) {
+#pragma unroll
+            for (int a = 0; a < N; ++a) {
+                A[tri(a, a)] = P.v0;  // cov_lookup(0) = vals[1] since bins[1] = 0 <= 0
+#pragma unroll
+                for (int b = 0; b < a; ++b)
+                    A[tri(a, b)] = cov_lookup<T, ONE>(radius<T>(sqdist<D>(jc[a], jc[b]), scale),
+                                                      tab, acc, P);
+            }
+            return;
+        }
+        using S = typename num<T>::sbits_t;
+        const T b0 = P.b0, bl = P.bl, v0 = P.v0, vl = P.vl;
 #pragma unroll
         for (int a = 0; a < N; ++a) {
-            A[tri(a, a)] = P.v0;  // cov_lookup(0) = vals[1] since bins[1] = 0 <= 0
+            A[tri(a, a)] = v0;
+            T r[N], rr[N];
+            int lo[N];
 #pragma unroll
-            for (int b = 0; b < a; ++b)
-                A[tri(a, b)] = cov_lookup<T, ONE>(radius<T>(sqdist<D>(jc[a], jc[b]), scale), tab,
-                                                  acc, P);
+            for (int b = 0; b < a; ++b) {
+                r[b] = radius<T>(sqdist<D>(jc[a], jc[b]), scale);
+                rr[b] = r[b] >= bl ? b0 : r[b];
+                const S d = (S)(num<T>::bits(rr[b]) - P.base);
+                const int cell = d < 0 ? 0 : (int)min((S)(d >> P.shift) + 1, (S)P.ucells);
+                lo[b] = acc[cell];
+            }
+#pragma unroll
+            for (int b = 0; b < a; ++b) lo[b] += rr[b] >= tab[lo[b]].x1 ? 1 : 0;
+#pragma unroll
+            for (int b = 0; b < a; ++b) {
+                const TabEnt<T> e = tab[lo[b]];
+                T v = num<T>::fma(e.slope, rr[b] - e.x0, e.y0);  // @fastmath y0 + slope*(r - x0)
+                v = r[b] >= bl ? vl : v;
+                A[tri(a, b)] = r[b] <= b0 ? v0 : v;
+            }
         }
     }
 

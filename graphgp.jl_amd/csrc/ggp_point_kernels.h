@@ -66,7 +66,7 @@ __device__ inline double factor_points(const uint32_t* __restrict__ coords,
         int32_t nb[K];
         blk.gather(coords, nbr, M, m, n0, nb);
         if (ANISO) blk.assemble_aniso(scale, an);
-        else blk.template assemble<ONE>(scale, s_tab, s_acc, P);
+        else blk.template assemble<ONE, true>(scale, s_tab, s_acc, P);
         blk.cholesky();
         const T s = blk.stddev();
         if (MODE & F_TERMS) {
@@ -488,13 +488,11 @@ k_pullback(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
         for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
     stage_table(s_tab, s_acc, g_tab, g_acc, P);
 
-    double ssum;
-    if (P.steps <= 1)
-        ssum = pullback_points<T, K, D, MODE, true>(coords, nbr, M, n0, scale, s_tab, s_acc, P, v,
-                                                    xi, vb, hist_partial, s_hist);
-    else
-        ssum = pullback_points<T, K, D, MODE, false>(coords, nbr, M, n0, scale, s_tab, s_acc, P, v,
-                                                     xi, vb, hist_partial, s_hist);
+    // The branch-free single-step lookups raise this kernel's register count past three
+    // wavefronts per SIMD, which costs more than they save: the general search throughout.
+    const double ssum = pullback_points<T, K, D, MODE, false>(coords, nbr, M, n0, scale, s_tab,
+                                                              s_acc, P, v, xi, vb, hist_partial,
+                                                              s_hist);
     __syncthreads();
     if (!PTS) {
         double* out = hist_partial + (size_t)blockIdx.x * P.nb;
