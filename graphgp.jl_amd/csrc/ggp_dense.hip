@@ -10,6 +10,7 @@
 // the same derivative evaluated in a parallel order.
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "ggp_internal.h"
 
@@ -264,7 +265,9 @@ __device__ inline void walk_accumulate(T (&acc)[4], const T* A, int n, int nt, i
 // out is given, into out (LDS). Called by wave 0.
 template <typename T>
 __device__ inline void walk_solve(T* A, int n, int i, int j, const T (*sA)[kTile + 1],
-                                  const T (*L)[kTile + 1], T (*out)[kTile + 1], int tid) {
+                                  const T (*L)[kTile + 1], const T* inv, T (*out)[kTile + 1],
+                                  int tid) {
+    constexpr bool kRsq = std::is_same<T, float>::value;
     const int r = tid & (kTile - 1);
     const bool live = tid < kTile && i * kTile + r < n;
     T a[kTile];
@@ -275,7 +278,7 @@ __device__ inline void walk_solve(T* A, int n, int i, int j, const T (*sA)[kTile
         T tt = a[jj];
 #pragma unroll
         for (int p = 0; p < jj; ++p) tt = num<T>::fma(-a[p], L[jj][p], tt);
-        a[jj] = tt / L[jj][jj];
+        a[jj] = kRsq ? tt * inv[jj] : tt / L[jj][jj];
     }
     if (live) {
         T* wp = A + (int64_t)(i * kTile + r) * n + j * kTile;
@@ -293,26 +296,44 @@ __host__ __device__ inline int walk_group_tasks(int g, int nt) {
 
 constexpr int kLtPitch = kTile + 4;  // transposed L rows, 16-byte aligned
 
+// sync = [ticket, tile flags[nt*nt], diagonal-partial flags[nt], sub-diagonal-partial flags[nt],
+// (padding to 8 bytes), reciprocal diagonal[nt*kTile] (f32 walker)]: ints before the last part.
+__host__ __device__ inline int dense_sync_flag_ints(int nt) { return (nt * nt + 2 * nt + 2) & ~1; }
+
 // Walker factor of the tile in sA into global tile (j, j) and, transposed, into Lt (LDS; zero
 // above the diagonal). Right-looking by columns: lane r owns row r; at step p the pivot and the
 // column values come from their lanes by readlane, and every entry (r, c), c > p, takes
-// fma(-L[r][p], L[c][p], .) — the unblocked left-looking chain in its order. Entries above the
-// diagonal are scratch (updated, never stored). Called by wave 0.
+// fma(-L[r][p], L[c][p], .). Entries above the diagonal are scratch (updated, never stored).
+// f64: L[p][p] = sqrt(pivot) and the column divided by it, the unblocked left-looking chain in
+// its order (the oracle's bits). f32: one reciprocal square root per column (v_rsq_f32, within
+// 1 ulp): L[p][p] = pivot * rsq and the column multiplied by rsq, which takes the square root
+// and the division off the column-to-column chain; rsq goes to inv (LDS) and dinv (global, for
+// the helpers' solves). Called by wave 0.
 template <typename T>
 __device__ inline void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1],
-                                     T (*Lt)[kLtPitch], int tid, int* info) {
+                                     T (*Lt)[kLtPitch], T* inv, T* dinv, int tid, int* info) {
+    constexpr bool kRsq = std::is_same<T, float>::value;
     const int r = tid & (kTile - 1);
     const bool live = tid < kTile && j * kTile + r < n;
     T a[kTile];
 #pragma unroll
     for (int cc = 0; cc < kTile; ++cc) a[cc] = sA[r][cc];
     bool bad = false;
+    T myinv = T(0);
 #pragma unroll
     for (int p = 0; p < kTile; ++p) {
         const T piv = bcast(a[p], p);
         bad = bad || !(piv > T(0));
-        const T d = num<T>::sqrt(piv);
-        const T l = a[p] / d;
+        T d, l;
+        if (kRsq) {
+            const T rs = (T)__builtin_amdgcn_rsqf((float)piv);
+            d = piv * rs;
+            l = a[p] * rs;
+            myinv = r == p ? rs : myinv;
+        } else {
+            d = num<T>::sqrt(piv);
+            l = a[p] / d;
+        }
         a[p] = r == p ? d : l;
 #pragma unroll
         for (int cc = p + 1; cc < kTile; ++cc) a[cc] = num<T>::fma(-a[p], bcast(a[p], cc), a[cc]);
@@ -322,10 +343,13 @@ __device__ inline void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1
 #pragma unroll
         for (int cc = 0; cc < kTile; ++cc)
             if (cc <= r) wp[cc] = a[cc];
+        if (kRsq) dinv[j * kTile + r] = myinv;
     }
-    if (tid < kTile)
+    if (tid < kTile) {
+        if (kRsq) inv[r] = myinv;
 #pragma unroll
         for (int cc = 0; cc < kTile; ++cc) Lt[cc][r] = cc <= r ? a[cc] : T(0);
+    }
     if (tid == 0 && bad) atomicOr(info, 1);
 }
 
@@ -337,7 +361,9 @@ __device__ inline void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1
 // and to P.
 template <typename T>
 __device__ inline void walk_solve_t(T* A, int n, int i, int j, const T (*sC)[kTile + 1],
-                                    const T (*Lt)[kLtPitch], T (*P)[kTile + 1], int tid) {
+                                    const T (*Lt)[kLtPitch], const T* inv, T (*P)[kTile + 1],
+                                    int tid) {
+    constexpr bool kRsq = std::is_same<T, float>::value;
     const int r = tid & (kTile - 1), h = tid >> 5;
     T a[16];
 #pragma unroll
@@ -345,7 +371,7 @@ __device__ inline void walk_solve_t(T* A, int n, int i, int j, const T (*sC)[kTi
 #pragma unroll
     for (int p = 0; p < kTile; ++p) {
         const int hp = p >> 4, up = p & 15;
-        const T x = a[up] / Lt[p][p];
+        const T x = kRsq ? a[up] * inv[p] : a[up] / Lt[p][p];
         const bool mine = h == hp;
         a[up] = mine ? x : a[up];
         const T xo = __shfl_xor(x, 32, 64);
@@ -381,7 +407,7 @@ __device__ inline void walk_load16(T (&v)[8], const T* A, int n, int i, int j, i
     }
 }
 
-// sync = [ticket, tile flags[nt*nt], diagonal-partial flags[nt], sub-diagonal-partial flags[nt]]
+// sync: the layout above (dense_sync_flag_ints).
 template <typename T>
 __global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, int n, int nt,
                                                            int ntasks, int* __restrict__ sync,
@@ -391,11 +417,13 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, in
     __shared__ T sC[kTile][kTile + 1];
     __shared__ T sP[kTile][kTile + 1];            // walker: L[j][j-1], then L[j+1][j]
     __shared__ __align__(16) T sLt[kTile][kLtPitch];  // walker: L[j][j] transposed
+    __shared__ T sInv[kTile];                         // f32: 1 / L[p][p] of the current tile
     __shared__ int s_task;
     int* ticket = sync;
     int* flags = sync + 1;
     int* pdf = flags + nt * nt;
     int* psf = pdf + nt;
+    T* dinv = reinterpret_cast<T*>(sync + dense_sync_flag_ints(nt));
     const int tid = threadIdx.x;
     const int c = tid & (kTile - 1), r0 = tid >> 5;
     if (tid == 0) s_task = atomicAdd(ticket, 1);
@@ -428,7 +456,7 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, in
             for (int q = 0; q < 4; ++q) sA[r0 + 8 * q][c] = acc[q];
             __syncthreads();
             if (w == 0) {
-                walk_factor_t(A, n, j, sA, sLt, tid, info);
+                walk_factor_t(A, n, j, sA, sLt, sInv, dinv, tid, info);
             } else if (sub && w <= 2) {
                 // sub-diagonal tile: partial sum over k < j-1 plus the k = j-1 term, into sC
                 const int R = 16 * (w - 1);
@@ -460,7 +488,7 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, in
                 __hip_atomic_store(&flags[j * nt + j], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
             if (sub) {
                 if (w == 0) {
-                    walk_solve_t(A, n, j + 1, j, sC, sLt, sP, tid);
+                    walk_solve_t(A, n, j + 1, j, sC, sLt, sInv, sP, tid);
                 } else if (w <= 2) {
                     // next diagonal partial sum into sA
                     const int R = 16 * (w - 1);
@@ -499,8 +527,10 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, in
                 sA[r][c] = acc[q];
                 sB[r][c] = (g * kTile + r < n && c <= r) ? A[(int64_t)(g * kTile + r) * n + g * kTile + c] : T(0);
             }
+            if (std::is_same<T, float>::value && tid < kTile)
+                sInv[tid] = g * kTile + tid < n ? dinv[g * kTile + tid] : T(1);
             __syncthreads();
-            if (tid < 64) walk_solve(A, n, i, g, sA, sB, (T(*)[kTile + 1])nullptr, tid);
+            if (tid < 64) walk_solve(A, n, i, g, sA, sB, sInv, (T(*)[kTile + 1])nullptr, tid);
             __syncthreads();
             if (tid == 0) {
                 __hip_atomic_store(&flags[i * nt + g], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -534,14 +564,14 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, in
 
 int dense_sync_ints(int n) {
     const int nt = (n + kTile - 1) / kTile;
-    return nt * nt + 2 * nt + 1;
+    return dense_sync_flag_ints(nt) + 2 * nt * kTile;  // + the reciprocal diagonal (<= f64)
 }
 
 template <typename T>
 void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st) {
     if (n <= 0) return;
     const int nt = (n + kTile - 1) / kTile;
-    launch_fill<int>(sync, 0, dense_sync_ints(n), st);
+    launch_fill<int>(sync, 0, dense_sync_flag_ints(nt), st);
     static const bool tiles = std::getenv("GGP_POTRF_TILES") != nullptr;
     if (tiles) {
         const int ntiles = nt * (nt + 1) / 2;
