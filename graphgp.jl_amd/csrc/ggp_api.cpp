@@ -329,6 +329,15 @@ T dense_aniso_diag(const Table<T>& tb) {
     return (g[0] * (one - zero) + g[i1 * nz] * zero) * (one - zero) + (g[j1] * (one - zero) + g[i1 * nz + j1] * zero) * zero;
 }
 
+// Workgroups of the dense factor's persistent launch: the walker plus helpers. The helpers take
+// tasks in dependency order and wait in place for their inputs, so their number sets how far
+// ahead of the walker the partial sums get started; half the CUs keeps every step's inputs
+// ready at n0 = 1000 (a quarter left the walker waiting on late partial sums).
+int dense_wgs(const ggp_graph* h) {
+    static const int env = std::getenv("GGP_DENSE_WGS") ? std::atoi(std::getenv("GGP_DENSE_WGS")) : 0;
+    return std::max(1, env > 0 ? env : h->ncu / 2);
+}
+
 // Dense factor with jitter escalation (src/dense.jl:46-67), synchronous; used after the first
 // in-op attempt reported a non-positive pivot.
 template <typename T>
@@ -344,7 +353,7 @@ int dense_retry(ggp_graph* h) {
     while (e <= T(1e-2)) {
         launch_fill<int>(h->info, 0, 1, h->s_main);
         dense_assemble<T>(h->g, tb, tp<T>(h->A), e * dmean, h->s_main);
-        dense_potrf<T>(tp<T>(h->A), n, h->info, h->dsync, std::max(1, h->ncu / 4), h->s_main);
+        dense_potrf<T>(tp<T>(h->A), n, h->info, h->dsync, dense_wgs(h), h->s_main);
         HC(hipMemcpyAsync(h->hinfo, h->info, sizeof(int), hipMemcpyDeviceToHost, h->s_main));
         HC(hipStreamSynchronize(h->s_main));
         if (*h->hinfo == 0) return 0;
@@ -361,7 +370,7 @@ void dense_factor_async(ggp_graph* h, hipStream_t st) {
     tstart(h, TM_DENSE, st);
     launch_fill<int>(h->info, 0, 1, st);
     dense_assemble<T>(h->g, table<T>(h), tp<T>(h->A), T(0), st);
-    dense_potrf<T>(tp<T>(h->A), (int)h->g.n0, h->info, h->dsync, std::max(1, h->ncu / 4), st);
+    dense_potrf<T>(tp<T>(h->A), (int)h->g.n0, h->info, h->dsync, dense_wgs(h), st);
     tstop(h, TM_DENSE, st);
 }
 
