@@ -59,10 +59,15 @@ struct ggp_graph {
     void *mv = nullptr, *sd = nullptr, *v = nullptr, *xt = nullptr, *vb = nullptr,
          *vbt = nullptr, *xg = nullptr, *A = nullptr, *tmp = nullptr;
     double* scal_partial = nullptr;  // nblk_factor (>= nblk_pull) doubles
-    double* dscal = nullptr;         // 8 doubles
-    double* hscal = nullptr;         // pinned host mirror of dscal
-    int* info = nullptr;
-    int* hinfo = nullptr;            // pinned host mirror of info
+    // Status block, one device allocation mirrored by one pinned host block so that an op
+    // fetches all of it with one copy: [0, 64) scalars, [64, 80) info, [80, 96) sweep errors.
+    void* dstat = nullptr;
+    void* hstat = nullptr;
+    double* dscal = nullptr;         // 8 doubles (dstat + 0)
+    double* hscal = nullptr;         // host mirror of dscal
+    int* info = nullptr;             // dstat + 64
+    int* hinfo = nullptr;            // host mirror of info
+    int* herr = nullptr;             // host mirror of the sweep error flags (dstat + 80)
     int* dsync = nullptr;            // dense Cholesky task counter and tile flags
     double* hist = nullptr;          // (nblk_pull + nw_dense) x nb
     int hist_nb = 0;
@@ -83,6 +88,8 @@ template <typename T> Table<T>& table(ggp_graph* h);
 template <> Table<float>& table<float>(ggp_graph* h) { return h->tf; }
 template <> Table<double>& table<double>(ggp_graph* h) { return h->td; }
 
+constexpr size_t kStatBytes = 96;
+
 int dmalloc(ggp_graph* h, void** p, size_t bytes) {
     if (bytes == 0) bytes = 16;
     hipError_t e = hipMalloc(p, bytes);
@@ -97,8 +104,7 @@ int dmalloc(ggp_graph* h, void** p, size_t bytes) {
 void free_all(ggp_graph* h) {
     for (void* p : h->owned) (void)hipFree(p);
     h->owned.clear();
-    if (h->hscal) (void)hipHostFree(h->hscal);
-    if (h->hinfo) (void)hipHostFree(h->hinfo);
+    if (h->hstat) (void)hipHostFree(h->hstat);
     if (h->s_main) (void)hipStreamDestroy(h->s_main);
     if (h->s_side) (void)hipStreamDestroy(h->s_side);
     if (h->ev_fork) (void)hipEventDestroy(h->ev_fork);
@@ -299,17 +305,15 @@ int join(ggp_graph* h) {
 }
 // Drain the main stream, release the user stream, and fetch info + scalars.
 int finish(ggp_graph* h, hipStream_t user) {
-    HC(hipMemcpyAsync(h->hinfo, h->info, sizeof(int), hipMemcpyDeviceToHost, h->s_main));
-    HC(hipMemcpyAsync(h->hinfo + 1, h->g.sweep_err, sizeof(int), hipMemcpyDeviceToHost, h->s_main));
-    HC(hipMemcpyAsync(h->hscal, h->dscal, 8 * sizeof(double), hipMemcpyDeviceToHost, h->s_main));
+    HC(hipMemcpyAsync(h->hstat, h->dstat, kStatBytes, hipMemcpyDeviceToHost, h->s_main));
     HC(hipGetLastError());
     tstop(h, TM_OP, h->s_main);
     HC(hipEventRecord(h->ev_user, h->s_main));
     HC(hipStreamWaitEvent(user, h->ev_user, 0));
     HC(hipStreamSynchronize(h->s_main));
     tcollect(h);
-    if (h->hinfo[1] & 4) {
-        h->hinfo[1] = 0;
+    if (h->herr[0] & 4) {
+        h->herr[0] = 0;
         (void)hipMemset(h->g.sweep_err, 0, sizeof(int));
         return fail(GGP_ERR_HIP, "level sweep: a wait for an input value timed out");
     }
@@ -993,17 +997,20 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     rc |= dmalloc(h, &h->tmp, (size_t)n0 * es);
     rc |= dmalloc(h, &h->A, (size_t)(n0 * n0) * es);
     rc |= dmalloc(h, (void**)&h->scal_partial, std::max(h->nblk_factor, h->nblk_pull) * 8);
-    rc |= dmalloc(h, (void**)&h->dscal, 8 * 8);
-    rc |= dmalloc(h, (void**)&h->info, 16);
+    rc |= dmalloc(h, &h->dstat, kStatBytes);
     rc |= dmalloc(h, (void**)&h->dsync, (size_t)dense_sync_ints((int)n0) * sizeof(int));
     rc |= dmalloc(h, (void**)&g.fwd_chunks, std::max<size_t>(fch.size(), 1) * sizeof(int4));
     rc |= dmalloc(h, (void**)&g.rev_chunks, std::max<size_t>(rch.size(), 1) * sizeof(int4));
     rc |= dmalloc(h, (void**)&g.sweep_ticket, 16);
-    rc |= dmalloc(h, (void**)&g.sweep_err, 16);
     if (rc) return bail(GGP_ERR_HIP);
-    if (hipHostMalloc((void**)&h->hscal, 8 * 8) != hipSuccess ||
-        hipHostMalloc((void**)&h->hinfo, 16) != hipSuccess)
+    if (hipHostMalloc(&h->hstat, kStatBytes) != hipSuccess)
         return bail(fail(GGP_ERR_HIP, "hipHostMalloc failed"));
+    h->dscal = static_cast<double*>(h->dstat);
+    h->info = reinterpret_cast<int*>(static_cast<char*>(h->dstat) + 64);
+    g.sweep_err = reinterpret_cast<int*>(static_cast<char*>(h->dstat) + 80);
+    h->hscal = static_cast<double*>(h->hstat);
+    h->hinfo = reinterpret_cast<int*>(static_cast<char*>(h->hstat) + 64);
+    h->herr = reinterpret_cast<int*>(static_cast<char*>(h->hstat) + 80);
     if (hipMemcpy(g.coords, coords_int.data(), (size_t)(N * D) * 4, hipMemcpyHostToDevice) != hipSuccess ||
         (relabel && hipMemcpy(g.i2t, i2t.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess) ||
         (relabel && hipMemcpy(g.i2tm, i2tm.data(), i2tm.size() * 4, hipMemcpyHostToDevice) != hipSuccess) ||
