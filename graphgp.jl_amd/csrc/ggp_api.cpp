@@ -372,9 +372,8 @@ int dense_retry(ggp_graph* h) {
 template <typename T>
 void dense_factor_async(ggp_graph* h, hipStream_t st) {
     tstart(h, TM_DENSE, st);
-    launch_fill<int>(h->info, 0, 1, st);
-    dense_assemble<T>(h->g, table<T>(h), tp<T>(h->A), T(0), st);
-    dense_potrf<T>(tp<T>(h->A), (int)h->g.n0, h->info, h->dsync, dense_wgs(h), st);
+    dense_assemble<T>(h->g, table<T>(h), tp<T>(h->A), T(0), st, h->info, h->dsync);
+    dense_potrf<T>(tp<T>(h->A), (int)h->g.n0, h->info, h->dsync, dense_wgs(h), st, true);
     tstop(h, TM_DENSE, st);
 }
 

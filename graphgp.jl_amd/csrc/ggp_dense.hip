@@ -23,7 +23,15 @@ template <typename T, int D, bool ANISO>
 __global__ void k_dense_assemble(T* __restrict__ A, const uint32_t* __restrict__ coords, int n,
                                  T scale, const TabEnt<T>* __restrict__ tab,
                                  const uint16_t* __restrict__ acc, const TabParams<T>* __restrict__ Pp, T diag_add,
-                                 AnisoArgs<T> an) {
+                                 AnisoArgs<T> an, int* __restrict__ z0, int n_z0,
+                                 int* __restrict__ z1, int n_z1) {
+    // Side job of the first workgroup: zero the factor's status and task flags (z0, z1), so the
+    // Cholesky launch follows this one directly.
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+        const int t = threadIdx.y * 16 + threadIdx.x;
+        for (int q = t; q < n_z0; q += 256) z0[q] = 0;
+        for (int q = t; q < n_z1; q += 256) z1[q] = 0;
+    }
     const int j = blockIdx.x * 16 + threadIdx.x;
     const int i = blockIdx.y * 16 + threadIdx.y;
     if (i >= n || j > i) return;
@@ -568,10 +576,10 @@ int dense_sync_ints(int n) {
 }
 
 template <typename T>
-void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st) {
+void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st, bool zeroed) {
     if (n <= 0) return;
     const int nt = (n + kTile - 1) / kTile;
-    launch_fill<int>(sync, 0, dense_sync_flag_ints(nt), st);
+    if (!zeroed) launch_fill<int>(sync, 0, dense_sync_flag_ints(nt), st);
     static const bool tiles = std::getenv("GGP_POTRF_TILES") != nullptr;
     if (tiles) {
         const int ntiles = nt * (nt + 1) / 2;
@@ -708,15 +716,17 @@ void dense_logdiag(const T* L, int n, double* out, hipStream_t st) {
 }
 
 template <typename T>
-void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStream_t st) {
+void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStream_t st,
+                    int* zero_info, int* zero_sync) {
+    const int nz1 = zero_sync ? dense_sync_flag_ints(cdiv((int)g.n0, kTile)) : 0;
     const int n = (int)g.n0;
     const dim3 grid(cdiv(n, 16), cdiv(n, 16)), blk(16, 16);
     const T scale = (T)g.scale;
     const bool an = tb.aniso.grid != nullptr;
 #define GGP_ASM(DD)                                                                             \
     do {                                                                                        \
-        if (an) hipLaunchKernelGGL((k_dense_assemble<T, DD, true>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso); \
-        else hipLaunchKernelGGL((k_dense_assemble<T, DD, false>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso); \
+        if (an) hipLaunchKernelGGL((k_dense_assemble<T, DD, true>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso, zero_info, zero_info ? 1 : 0, zero_sync, nz1); \
+        else hipLaunchKernelGGL((k_dense_assemble<T, DD, false>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso, zero_info, zero_info ? 1 : 0, zero_sync, nz1); \
     } while (0)
     switch (g.D) {
         case 2: GGP_ASM(2); break;
@@ -1166,8 +1176,9 @@ void dense_grad_points_invloss(const Graph& g, const Table<T>& tb, const T* alph
 }
 
 #define GGP_DENSE_INST(T)                                                                      \
-    template void dense_assemble<T>(const Graph&, const Table<T>&, T*, T, hipStream_t);        \
-    template void dense_potrf<T>(T*, int, int*, int*, int, hipStream_t);                                  \
+    template void dense_assemble<T>(const Graph&, const Table<T>&, T*, T, hipStream_t, int*,   \
+                                    int*);                                                     \
+    template void dense_potrf<T>(T*, int, int*, int*, int, hipStream_t, bool);                            \
     template void dense_trmv<T>(const T*, int, const T*, T*, hipStream_t);                     \
     template void dense_trmv_t<T>(const T*, int, const T*, T*, hipStream_t);                   \
     template void dense_trsv<T>(const T*, int, const T*, T*, hipStream_t);                     \

@@ -173,13 +173,17 @@ void launch_points_out(T* out, const double* dp, const double* dpd, int64_t N, i
 void launch_sqrt_check(uint32_t b0, uint32_t count, unsigned long long* bad, hipStream_t st);
 
 // Dense first layer (ggp_dense.hip). Matrices are n x n row-major; L lower.
+// zero_info / zero_sync (optional): zeroed by the same launch (*zero_info and the flag part of
+// a dense_potrf sync workspace), so that dense_potrf(..., zeroed = true) can follow directly.
 template <typename T>
-void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStream_t st);
+void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStream_t st,
+                    int* zero_info = nullptr, int* zero_sync = nullptr);
 // Cholesky in place (lower), one persistent launch of at most max_wg workgroups; sync is a
 // workspace of dense_sync_ints(n) ints. *info: bit 0 = non-positive pivot, bit 1 = a wait ran
 // past its bound (the result is then invalid).
 template <typename T>
-void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st);
+void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st,
+                 bool zeroed = false);
 int dense_sync_ints(int n);
 template <typename T>
 void dense_trmv(const T* L, int n, const T* x, T* y, hipStream_t st);
