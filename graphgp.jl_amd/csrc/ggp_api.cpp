@@ -54,7 +54,9 @@ struct ggp_graph {
     unsigned nblk_factor = 1024, nblk_pull = 512;
     int nw_dense = 256;
     hipStream_t s_main = nullptr, s_side = nullptr;
+    hipStream_t s_rev = nullptr;  // generate_grad_vals: the reverse sweep beside the forward chain
     hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_user = nullptr;
+    hipEvent_t ev_fac = nullptr, ev_rev = nullptr;
     // workspaces (element type T = dtype)
     void *mv = nullptr, *sd = nullptr, *v = nullptr, *xt = nullptr, *vb = nullptr,
          *vbt = nullptr, *xg = nullptr, *A = nullptr, *tmp = nullptr;
@@ -107,6 +109,9 @@ void free_all(ggp_graph* h) {
     if (h->hstat) (void)hipHostFree(h->hstat);
     if (h->s_main) (void)hipStreamDestroy(h->s_main);
     if (h->s_side) (void)hipStreamDestroy(h->s_side);
+    if (h->s_rev) (void)hipStreamDestroy(h->s_rev);
+    if (h->ev_fac) (void)hipEventDestroy(h->ev_fac);
+    if (h->ev_rev) (void)hipEventDestroy(h->ev_rev);
     if (h->ev_fork) (void)hipEventDestroy(h->ev_fork);
     if (h->ev_join) (void)hipEventDestroy(h->ev_join);
     if (h->ev_user) (void)hipEventDestroy(h->ev_user);
@@ -652,18 +657,25 @@ int op_grad_vals(ggp_graph* h, int mode, int dkind, const T* in1, const T* in2, 
         if (int rc = fork(h)) return rc;
         dense_factor_async<T>(h, h->s_side);
         HC(hipEventRecord(h->ev_join, h->s_side));  // the factor is done
-        // L^-1 needs only the factor: it runs beside both sweeps
-        dense_inverse<T>(tp<T>(h->A), (int)g.n0, h->W, h->C, h->s_side);
         launch_gather<T>(xt, in1, g.idx, g.N, h->s_main);
         launch_gather<T>(vbt, in2, g.idx, g.N, h->s_main);
         launch_sweep_prep<T>(g, v, vb, h->s_main);
         zero_tail<T>(h, v, h->s_main);
         factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr, nullptr);
-        // the sweeps need v[0:n0] = L xi[0:n0]: wait for the factor, not for the inverse
+        // The reverse sweep needs only mean_vec / std and the cotangent: it runs on its own
+        // stream beside the dense factor and the forward chain.
+        HC(hipEventRecord(h->ev_fac, h->s_main));
+        HC(hipStreamWaitEvent(h->s_rev, h->ev_fac, 0));
+        sweep_reverse<T>(h, vb, vbt, nullptr, h->s_rev, true);
+        HC(hipEventRecord(h->ev_rev, h->s_rev));
+        // L^-1 needs only the factor: it runs beside both sweeps (enqueued after the main
+        // stream's first launches, which it does not hold up)
+        dense_inverse<T>(tp<T>(h->A), (int)g.n0, h->W, h->C, h->s_side);
+        // the forward sweep needs v[0:n0] = L xi[0:n0]: wait for the factor, not for the inverse
         HC(hipStreamWaitEvent(h->s_main, h->ev_join, 0));
         dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_main);
         sweep_forward<T>(h, v, xt, g.n0, h->s_main, true);
-        sweep_reverse<T>(h, vb, vbt, nullptr, h->s_main, true);
+        HC(hipStreamWaitEvent(h->s_main, h->ev_rev, 0));
         pull_v = v;
         if (int rc = fork(h)) return rc;
         dense_grad<T>(h, DG_GENERATE, h->s_side, true);
@@ -1023,6 +1035,9 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
         return bail(fail(GGP_ERR_HIP, "hipMemcpy of the graph failed"));
     if (hipStreamCreateWithFlags(&h->s_main, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&h->s_side, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&h->s_rev, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&h->ev_fac, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&h->ev_rev, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&h->ev_fork, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&h->ev_join, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&h->ev_user, hipEventDisableTiming) != hipSuccess)

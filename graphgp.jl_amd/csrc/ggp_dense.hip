@@ -596,26 +596,95 @@ void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st, 
 }
 
 // ---- triangular products and solves ---------------------------------------------------------
+// Products with L and L^T. One workgroup per kTvRows outputs: all 256 threads stage the
+// entries those outputs use (and x) in LDS with coalesced loads, kTvCols at a time; lane r then
+// runs output r's fma chain from LDS in the serial order below. Every output keeps the chain of
+// a row-by-row loop, so the result is that loop's, bit for bit. Acc is the accumulation type
+// (T, or double for the f64 dense cotangents).
+constexpr int kTvRows = 4, kTvCols = 1024, kTvLoads = kTvRows * kTvCols / 256;
+
+template <typename A>
+__device__ inline A fma_acc(A a, A b, A c) { return num<A>::fma(a, b, c); }
+
+// acc chained over c in [c0, c1) of row r of the staged tile, 16 entries per batch (the batch's
+// LDS reads are issued together; row starts are 16-byte aligned, so aligned batches vectorise).
+template <typename T, typename Acc>
+__device__ inline Acc tv_chain(const T* __restrict__ row, const T* __restrict__ sx, int c0, int c1,
+                               Acc acc) {
+    int c = c0;
+    for (; c < c1 && (c & 3); ++c) acc = fma_acc<Acc>((Acc)row[c], (Acc)sx[c], acc);
+    for (; c + 16 <= c1; c += 16) {
+        T a[16], b[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) { a[u] = row[c + u]; b[u] = sx[c + u]; }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc = fma_acc<Acc>((Acc)a[u], (Acc)b[u], acc);
+    }
+    for (; c < c1; ++c) acc = fma_acc<Acc>((Acc)row[c], (Acc)sx[c], acc);
+    return acc;
+}
+
 // y = L x (src/dense.jl:118): row i accumulates j = 0..i.
-template <typename T>
-__global__ void k_trmv(const T* __restrict__ L, int n, const T* __restrict__ x, T* __restrict__ y) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const T* row = L + (int64_t)i * n;
-    T acc = T(0);
-#pragma unroll 16
-    for (int j = 0; j <= i; ++j) acc = num<T>::fma(row[j], x[j], acc);
-    y[i] = acc;
+template <typename T, typename Acc, typename Out>
+__global__ void __launch_bounds__(256) k_trmv(const T* __restrict__ L, int n,
+                                              const T* __restrict__ x, Out* __restrict__ y) {
+    constexpr int pitch = kTvCols + 16 / (int)sizeof(T);
+    __shared__ __align__(16) T sL[kTvRows * pitch];
+    __shared__ __align__(16) T sx[kTvCols];
+    const int i0 = blockIdx.x * kTvRows, tid = threadIdx.x;
+    const int nr = min(kTvRows, n - i0), jmax = i0 + nr;
+    Acc acc = Acc(0);
+    for (int j0 = 0; j0 < jmax; j0 += kTvCols) {
+        const int w = min(kTvCols, jmax - j0);
+        T t[kTvLoads];
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kTvLoads; ++q) {
+            const int e = q * 256 + tid, r = e / kTvCols, c = e % kTvCols;
+            t[q] = (r < nr && c < w) ? L[(int64_t)(i0 + r) * n + j0 + c] : T(0);
+        }
+        for (int c = tid; c < w; c += 256) sx[c] = x[j0 + c];
+#pragma unroll
+        for (int q = 0; q < kTvLoads; ++q) {
+            const int e = q * 256 + tid;
+            sL[(e / kTvCols) * pitch + e % kTvCols] = t[q];
+        }
+        __syncthreads();
+        if (tid < nr)
+            acc = tv_chain<T, Acc>(sL + tid * pitch, sx, 0, min(i0 + tid + 1, j0 + w) - j0, acc);
+    }
+    if (tid < nr) y[i0 + tid] = (Out)acc;
 }
 // y = L^T x (src/grad.jl:457, 493): entry i accumulates j = i..n-1.
-template <typename T>
-__global__ void k_trmv_t(const T* __restrict__ L, int n, const T* __restrict__ x, T* __restrict__ y) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    T acc = T(0);
-#pragma unroll 16
-    for (int j = i; j < n; ++j) acc = num<T>::fma(L[(int64_t)j * n + i], x[j], acc);
-    y[i] = acc;
+template <typename T, typename Acc, typename Out>
+__global__ void __launch_bounds__(256) k_trmv_t(const T* __restrict__ L, int n,
+                                                const T* __restrict__ x, Out* __restrict__ y) {
+    constexpr int pitch = kTvCols + 16 / (int)sizeof(T);
+    __shared__ __align__(16) T sL[kTvRows * pitch];
+    __shared__ __align__(16) T sx[kTvCols];
+    const int i0 = blockIdx.x * kTvRows, tid = threadIdx.x;
+    const int nr = min(kTvRows, n - i0);
+    Acc acc = Acc(0);
+    for (int j0 = i0; j0 < n; j0 += kTvCols) {
+        const int w = min(kTvCols, n - j0);
+        T t[kTvLoads];
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kTvLoads; ++q) {
+            const int e = q * 256 + tid, c = e / kTvRows, r = e % kTvRows;
+            t[q] = (r < nr && c < w) ? L[(int64_t)(j0 + c) * n + i0 + r] : T(0);
+        }
+        for (int c = tid; c < w; c += 256) sx[c] = x[j0 + c];
+#pragma unroll
+        for (int q = 0; q < kTvLoads; ++q) {
+            const int e = q * 256 + tid;
+            sL[(e % kTvRows) * pitch + e / kTvRows] = t[q];
+        }
+        __syncthreads();
+        if (tid < nr)
+            acc = tv_chain<T, Acc>(sL + tid * pitch, sx, max(i0 + tid - j0, 0), w, acc);
+    }
+    if (tid < nr) y[i0 + tid] = (Out)acc;
 }
 
 // x = L \ b (src/dense.jl:134), one workgroup: 32-row diagonal blocks solved by wave 0 with
@@ -696,11 +765,11 @@ __global__ void k_logdiag(const T* __restrict__ L, int n, double* __restrict__ o
 
 template <typename T>
 void dense_trmv(const T* L, int n, const T* x, T* y, hipStream_t st) {
-    hipLaunchKernelGGL((k_trmv<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, L, n, x, y);
+    hipLaunchKernelGGL((k_trmv<T, T, T>), dim3(cdiv(n, kTvRows)), dim3(256), 0, st, L, n, x, y);
 }
 template <typename T>
 void dense_trmv_t(const T* L, int n, const T* x, T* y, hipStream_t st) {
-    hipLaunchKernelGGL((k_trmv_t<T>), dim3(cdiv(n, 64)), dim3(64), 0, st, L, n, x, y);
+    hipLaunchKernelGGL((k_trmv_t<T, T, T>), dim3(cdiv(n, kTvRows)), dim3(256), 0, st, L, n, x, y);
 }
 template <typename T>
 void dense_trsv(const T* L, int n, const T* b, T* x, hipStream_t st) {
@@ -941,20 +1010,6 @@ static void dense_inverse64(const T* L, int n, double* W, double* S, hipStream_t
     }
 }
 
-// u = L^T vb (double), h/Q prefix pass: Q[a][j] = u[a] (sum_{j<=b<a} xi[b] W[b][j] + xi[a]W[a][j]/2)
-template <typename T>
-__global__ void __launch_bounds__(64) k_ltv64(const T* __restrict__ L, int n,
-                                              const T* __restrict__ vb, double* __restrict__ u) {
-    // u[a] += sum over the 64 rows of this block's row chunk (rows >= a) of L[i][a] vb[i]
-    const int a = blockIdx.x * 64 + threadIdx.x;
-    const int i0 = blockIdx.y * 64;
-    if (a >= n || i0 + 63 < (int)(blockIdx.x * 64)) return;
-    double s = 0.0;
-    const int i1 = min(n, i0 + 64);
-#pragma unroll 8
-    for (int i = max(i0, a); i < i1; ++i) s = __builtin_fma((double)L[(int64_t)i * n + a], (double)vb[i], s);
-    atomicAdd(&u[a], s);
-}
 // Q[a][j] = u[a] (h_j(a) + xi[a] W[a][j] / 2), h_j(a) = sum_{b<a} xi[b] W[b][j] (W is lower
 // triangular, so rows above j add zeros). Workgroup = 32 columns x 8 row chunks: chunk sums,
 // an exclusive prefix over the chunks in LDS, then the running sum within each chunk.
@@ -1081,8 +1136,9 @@ void dense_grad_generate(const Graph& g, const Table<T>& tb, const T* L, const T
                          double* hist_partial, int nw, bool inverse_ready, hipStream_t st) {
     const int n = (int)g.n0;
     if (!inverse_ready) dense_inverse64(L, n, W, C, st);
-    launch_fill<double>(u, 0.0, n, st);
-    hipLaunchKernelGGL((k_ltv64<T>), dim3(cdiv(n, 64), cdiv(n, 64)), dim3(64), 0, st, L, n, vb, u);
+    // u = L^T vb in double (rows i >= a, increasing i)
+    hipLaunchKernelGGL((k_trmv_t<T, double, double>), dim3(cdiv(n, kTvRows)), dim3(256), 0, st, L,
+                       n, vb, u);
     hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 32)), dim3(256), 0, st, W, n, xi, u, Q);
     launch_gemm<double>({gemm_job(W, n, 1, Q, n, C, n, n, n, n, GK_FROM_I | GK_FROM_J, 1.0)}, st);
     launch_dense_scatter<T, DM_GENERATE>(g, tb, C, nullptr, hist_partial, nw, st);
