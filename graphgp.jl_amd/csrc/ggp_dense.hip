@@ -809,16 +809,17 @@ void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStr
 // ---- dense cotangents (f64) -----------------------------------------------------------------
 // ---- f64 matrix-core GEMM ---------------------------------------------------------------------
 // C = alpha * op(A) * B for a batch of independent jobs, on v_mfma_f64_16x16x4f64. Each
-// workgroup owns a 64x64 tile of one job's C; its four wavefronts own 32x32 quarters (2 x 2
-// MFMA blocks). k advances in 32-deep chunks staged in LDS, the next chunk prefetched into
-// registers while the current one is multiplied. Operand layout of the instruction: A[i][k] in
-// lane i + 16k, B[k][j] in lane j + 16k; D[i][j] in lane j + 16(i mod 4), element i / 4.
+// workgroup owns a TM x TM tile of one job's C (TM = 64, or 32 for batches with too few 64-tiles
+// to fill the chip); its four wavefronts own TM/2 x TM/2 quarters (2 x 2 or 1 x 1 MFMA blocks).
+// k advances in 32-deep chunks staged in LDS, the next chunk prefetched into registers while the
+// current one is multiplied. Operand layout of the instruction: A[i][k] in lane i + 16k, B[k][j]
+// in lane j + 16k; D[i][j] in lane j + 16(i mod 4), element i / 4.
 //
 // Triangular operands: flags restrict k to the part that can be non-zero for the tile
-// (GK_FROM_I: k >= i0, GK_FROM_J: k >= j0, GK_TO_I: k < i0 + 64); entries the flags skip are zero
+// (GK_FROM_I: k >= i0, GK_FROM_J: k >= j0, GK_TO_I: k < i0 + TM); entries the flags skip are zero
 // in the operand, so the product is unchanged. GK_LOWER skips tiles strictly above the diagonal.
 typedef double f64x4 __attribute__((ext_vector_type(4)));
-constexpr int kGM = 64, kGK = 32, kGemmJobs = 24;
+constexpr int kGK = 32, kGemmJobs = 24;
 enum GemmFlags { GK_FROM_I = 1, GK_FROM_J = 2, GK_TO_I = 4, GK_LOWER = 8 };
 struct GemmJob {
     const void* A;
@@ -836,55 +837,56 @@ struct GemmBatch {
     int njobs;
 };
 
-template <typename TA>
+template <typename TA, int TM>
 __global__ void __launch_bounds__(256) k_gemm64(GemmBatch batch) {
-    __shared__ double sA[kGK][kGM + 2];
-    __shared__ double sB[kGK][kGM + 2];
+    constexpr int WQ = TM / 2, NB = WQ / 16, NF = TM * kGK / 256;
+    __shared__ double sA[kGK][TM + 2];
+    __shared__ double sB[kGK][TM + 2];
     int jb = 0;
     while (jb + 1 < batch.njobs && batch.job[jb + 1].tile0 <= (int)blockIdx.x) ++jb;
     const GemmJob& g = batch.job[jb];
     const int t = (int)blockIdx.x - g.tile0;
-    const int i0 = (t / g.tiles_n) * kGM, j0 = (t % g.tiles_n) * kGM;
+    const int i0 = (t / g.tiles_n) * TM, j0 = (t % g.tiles_n) * TM;
     if ((g.flags & GK_LOWER) && j0 > i0) return;
     int ks = 0, ke = g.K;
     if (g.flags & GK_FROM_I) ks = max(ks, i0);
     if (g.flags & GK_FROM_J) ks = max(ks, j0);
-    if (g.flags & GK_TO_I) ke = min(ke, i0 + kGM);
+    if (g.flags & GK_TO_I) ke = min(ke, i0 + TM);
     ks = (ks / kGK) * kGK;
     const TA* __restrict__ A = static_cast<const TA*>(g.A);
     const double* __restrict__ B = g.B;
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
-    const int wr = (w >> 1) * 32, wc = (w & 1) * 32;
-    f64x4 acc[2][2];
+    const int wr = (w >> 1) * WQ, wc = (w & 1) * WQ;
+    f64x4 acc[NB][NB];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < NB; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = (f64x4){0.0, 0.0, 0.0, 0.0};
-    // register staging of one chunk: 8 A and 8 B entries per thread
-    double ra[8], rb[8];
+        for (int b = 0; b < NB; ++b) acc[a][b] = (f64x4){0.0, 0.0, 0.0, 0.0};
+    // register staging of one chunk: NF A and NF B entries per thread
+    double ra[NF], rb[NF];
     auto fetch = [&](int k0) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
+        for (int q = 0; q < NF; ++q) {
             const int e = tid + 256 * q;
             int ii, kk;
-            if (g.atrans) { kk = e / kGM; ii = e % kGM; } else { ii = e / kGK; kk = e % kGK; }
+            if (g.atrans) { kk = e / TM; ii = e % TM; } else { ii = e / kGK; kk = e % kGK; }
             const int gi = i0 + ii, gk = k0 + kk;
             ra[q] = (gi < g.M && gk < ke)
                         ? (double)(g.atrans ? A[(int64_t)gk * g.lda + gi] : A[(int64_t)gi * g.lda + gk])
                         : 0.0;
-            const int kb = e / kGM, jj = e % kGM;
+            const int kb = e / TM, jj = e % TM;
             const int gj = j0 + jj, gkb = k0 + kb;
             rb[q] = (gj < g.N && gkb < ke) ? B[(int64_t)gkb * g.ldb + gj] : 0.0;
         }
     };
     auto stash = [&]() {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
+        for (int q = 0; q < NF; ++q) {
             const int e = tid + 256 * q;
             int ii, kk;
-            if (g.atrans) { kk = e / kGM; ii = e % kGM; } else { ii = e / kGK; kk = e % kGK; }
+            if (g.atrans) { kk = e / TM; ii = e % TM; } else { ii = e / kGK; kk = e % kGK; }
             sA[kk][ii] = ra[q];
-            sB[e / kGM][e % kGM] = rb[q];
+            sB[e / TM][e % TM] = rb[q];
         }
     };
     if (ks < ke) fetch(ks);
@@ -896,18 +898,22 @@ __global__ void __launch_bounds__(256) k_gemm64(GemmBatch batch) {
 #pragma unroll
         for (int s = 0; s < kGK / 4; ++s) {
             const int kr = s * 4 + (l >> 4);
-            const double a0 = sA[kr][wr + (l & 15)], a1 = sA[kr][wr + 16 + (l & 15)];
-            const double b0 = sB[kr][wc + (l & 15)], b1 = sB[kr][wc + 16 + (l & 15)];
-            acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
+            double av[NB], bv[NB];
+#pragma unroll
+            for (int a = 0; a < NB; ++a) av[a] = sA[kr][wr + 16 * a + (l & 15)];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) bv[b] = sB[kr][wc + 16 * b + (l & 15)];
+#pragma unroll
+            for (int a = 0; a < NB; ++a)
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[a], bv[b], acc[a][b], 0, 0, 0);
         }
     }
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < NB; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int i = i0 + wr + 16 * a + (l >> 4) + 4 * v;
@@ -916,21 +922,30 @@ __global__ void __launch_bounds__(256) k_gemm64(GemmBatch batch) {
             }
 }
 
-// Launch a list of jobs (split into batches of kGemmJobs).
+// Launch a list of jobs (split into batches of kGemmJobs). A batch whose 64 x 64 tiles would
+// give fewer than kGemmFill workgroups runs on 32 x 32 tiles (4x the workgroups).
+constexpr int kGemmFill = 512;
 template <typename TA>
 static void launch_gemm(std::vector<GemmJob> jobs, hipStream_t st) {
     for (size_t s = 0; s < jobs.size(); s += kGemmJobs) {
+        const int nj = (int)std::min<size_t>(kGemmJobs, jobs.size() - s);
+        int t64 = 0;
+        for (int q = 0; q < nj; ++q)
+            t64 += (int)(cdiv(jobs[s + q].M, 64) * cdiv(jobs[s + q].N, 64));
+        const int tm = t64 < kGemmFill ? 32 : 64;
         GemmBatch b{};
         int tiles = 0;
-        b.njobs = (int)std::min<size_t>(kGemmJobs, jobs.size() - s);
-        for (int q = 0; q < b.njobs; ++q) {
+        b.njobs = nj;
+        for (int q = 0; q < nj; ++q) {
             GemmJob j = jobs[s + q];
-            j.tiles_n = (j.N + kGM - 1) / kGM;
+            j.tiles_n = (j.N + tm - 1) / tm;
             j.tile0 = tiles;
-            tiles += ((j.M + kGM - 1) / kGM) * j.tiles_n;
+            tiles += ((j.M + tm - 1) / tm) * j.tiles_n;
             b.job[q] = j;
         }
-        if (tiles > 0) hipLaunchKernelGGL((k_gemm64<TA>), dim3(tiles), dim3(256), 0, st, b);
+        if (tiles <= 0) continue;
+        if (tm == 32) hipLaunchKernelGGL((k_gemm64<TA, 32>), dim3(tiles), dim3(256), 0, st, b);
+        else hipLaunchKernelGGL((k_gemm64<TA, 64>), dim3(tiles), dim3(256), 0, st, b);
     }
 }
 
