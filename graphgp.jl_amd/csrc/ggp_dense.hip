@@ -343,8 +343,13 @@ __device__ inline void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1
             l = a[p] / d;
         }
         a[p] = r == p ? d : l;
+        // column p from its lanes first (separate scalars: no read-after-readlane stall per
+        // entry), then the updates
+        T col[kTile];
 #pragma unroll
-        for (int cc = p + 1; cc < kTile; ++cc) a[cc] = num<T>::fma(-a[p], bcast(a[p], cc), a[cc]);
+        for (int cc = p + 1; cc < kTile; ++cc) col[cc] = bcast(a[p], cc);
+#pragma unroll
+        for (int cc = p + 1; cc < kTile; ++cc) a[cc] = num<T>::fma(-a[p], col[cc], a[cc]);
     }
     if (live) {
         T* wp = A + (int64_t)(j * kTile + r) * n + j * kTile;
