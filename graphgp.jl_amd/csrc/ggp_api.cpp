@@ -1118,6 +1118,27 @@ int ggp_selftest_sqrt_f32(uint32_t first_bits, uint32_t count, uint64_t* mismatc
     return 0;
 }
 
+int ggp_selftest_div(int32_t dtype, uint64_t first, uint64_t count, uint32_t per_divisor,
+                     uint64_t seed, uint64_t* mismatches) {
+    if (!mismatches) return fail(GGP_ERR_ARG, "null argument");
+    if (dtype != GGP_F32 && dtype != GGP_F64) return fail(GGP_ERR_ARG, "dtype must be GGP_F32 or GGP_F64");
+    if (dtype == GGP_F32 && (first > 0xffffffffull || count > 0x100000000ull - first))
+        return fail(GGP_ERR_ARG, "f32 divisor range past the 32-bit patterns");
+    unsigned long long* d = nullptr;
+    HC(hipMalloc((void**)&d, sizeof(*d)));
+    hipError_t e = hipMemset(d, 0, sizeof(*d));
+    if (e == hipSuccess && count && per_divisor) {
+        ggp::launch_div_check(dtype == GGP_F64, first, count, per_divisor, seed, d, nullptr);
+        e = hipGetLastError();
+    }
+    unsigned long long hbad = 0;
+    if (e == hipSuccess) e = hipMemcpy(&hbad, d, sizeof(hbad), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return fail(GGP_ERR_HIP, std::string("division self-test: ") + hipGetErrorString(e));
+    *mismatches = hbad;
+    return 0;
+}
+
 int ggp_kernel_timer_read(const ggp_graph* h, const char* name, double* total_ms, int64_t* count) {
     if (!h || !name) return fail(GGP_ERR_ARG, "null argument");
     for (int t = 0; t < TM_COUNT; ++t)

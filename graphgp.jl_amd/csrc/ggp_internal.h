@@ -171,6 +171,10 @@ void launch_points_out(T* out, const double* dp, const double* dpd, int64_t N, i
 
 // Self-check of the lattice square root (sqrt_rn_f32) over bit patterns [b0, b0 + count).
 void launch_sqrt_check(uint32_t b0, uint32_t count, unsigned long long* bad, hipStream_t st);
+// Self-check of div_rcp against the IEEE division (f32: divisor bit patterns [b0, b0 + count);
+// f64: count random divisors), `per` numerators per divisor.
+void launch_div_check(int f64, uint64_t b0, uint64_t count, uint32_t per, uint64_t seed,
+                      unsigned long long* bad, hipStream_t st);
 
 // Dense first layer (ggp_dense.hip). Matrices are n x n row-major; L lower.
 // zero_info / zero_sync (optional): zeroed by the same launch (*zero_info and the flag part of

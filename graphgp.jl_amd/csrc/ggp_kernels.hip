@@ -267,6 +267,53 @@ void launch_points_out(T* out, const double* dp, const double* dpd, int64_t N, i
                            dpd, N, D, n_dense, map);
 }
 
+// Self-check of div_rcp against the IEEE division. f32: every divisor bit pattern in
+// [b0, b0 + count), each with `per` numerators; f64: `count` random divisors in [2^-60, 2^60).
+// Numerators: random sign and significand, exponent uniform over 2^-100 .. 2^100 (f32) or
+// 2^-900 .. 2^900 (f64), and zero.
+__device__ inline uint64_t mix64(uint64_t x) {
+    x += 0x9e3779b97f4a7c15ull;
+    x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+    x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+    return x ^ (x >> 31);
+}
+__global__ void __launch_bounds__(256) k_div_check(int f64, uint64_t b0, uint64_t count,
+                                                   uint32_t per, uint64_t seed,
+                                                   unsigned long long* bad) {
+    unsigned long long nbad = 0;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+        if (!f64) {
+            const float d = __uint_as_float((uint32_t)(b0 + i));
+            const float y = 1.0f / d;
+            for (uint32_t u = 0; u < per; ++u) {
+                const uint64_t h = mix64(seed ^ (i * 0x100000001b3ull + u));
+                const uint32_t e = 27u + (uint32_t)((h >> 32) % 201u);  // 2^-100 .. 2^100
+                const uint32_t bits = (uint32_t)(h & 0x807fffffu) | (e << 23);
+                const float t = u == 0 ? 0.0f : __uint_as_float(bits);
+                nbad += __float_as_uint(ggp::div_rcp(t, d, y)) != __float_as_uint(t / d);
+            }
+        } else {
+            const uint64_t hd = mix64(seed + i);
+            const uint64_t ed = 963u + (hd >> 52) % 121u;  // 2^-60 .. 2^60
+            const double d = __longlong_as_double((long long)((hd & 0x000fffffffffffffull) | (ed << 52)));
+            const double y = 1.0 / d;
+            for (uint32_t u = 0; u < per; ++u) {
+                const uint64_t h = mix64(hd ^ (u * 0x9e3779b97f4a7c15ull));
+                const uint64_t e = 123u + (h >> 52) % 1801u;  // 2^-900 .. 2^900
+                const uint64_t bits = (h & 0x800fffffffffffffull) | (e << 52);
+                const double t = u == 0 ? 0.0 : __longlong_as_double((long long)bits);
+                nbad += __double_as_longlong(ggp::div_rcp(t, d, y)) != __double_as_longlong(t / d);
+            }
+        }
+    }
+    if (nbad) atomicAdd(bad, nbad);
+}
+void launch_div_check(int f64, uint64_t b0, uint64_t count, uint32_t per, uint64_t seed,
+                      unsigned long long* bad, hipStream_t st) {
+    hipLaunchKernelGGL(k_div_check, dim3(4096), dim3(256), 0, st, f64, b0, count, per, seed, bad);
+}
+
 // Self-check of sqrt_rn_f32 against the correctly rounded sqrtf over `count` consecutive bit
 // patterns from b0; *bad receives the number of differing results.
 __global__ void __launch_bounds__(256) k_sqrt_check(uint32_t b0, uint32_t count,

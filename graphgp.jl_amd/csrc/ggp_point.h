@@ -36,6 +36,19 @@ template <> struct num<double> {
     __device__ static inline bits_t bits(double a) { return (bits_t)__double_as_longlong(a); }
 };
 
+// t / d rounded once, given y = RN(1/d) (one IEEE division per divisor): q0 = t*y lies within
+// an ulp of t/d, the remainder t - d*q0 is exact in one fma, and q0 + (t - d*q0)*y rounded once
+// is the correctly rounded quotient (Markstein's correction step, as in the IA-64 division
+// sequences). It equals the IEEE division whenever the remainder is representable and nothing
+// overflows: t = 0, or |t| >= 2^-103 (f32; 2^-970 in f64) with a normal quotient. A nonzero
+// |t| below that (reachable only by cancelling covariance entries to 2^-100 of their size) may
+// differ in the last bit of a subnormal-range quotient. ggp_selftest_div checks it on the device.
+template <typename T>
+__device__ inline T div_rcp(T t, T d, T y) {
+    const T q0 = t * y;
+    return num<T>::fma(num<T>::fma(-q0, d, t), y, q0);
+}
+
 // ---- cross-lane moves (wave-uniform lane index; call from wave-uniform control flow) --------
 // bcast: the value of x in `lane`, for every lane. put: x with `lane`'s value replaced by v
 // (me = the calling lane).
@@ -295,6 +308,7 @@ struct Block {
     static constexpr int NT = N * (N + 1) / 2;
     uint32_t jc[N][D];  // joint lattice coords: rows 0..K-1 the neighbours, row K the point
     T A[NT];            // covariance, then its Cholesky factor (packed lower)
+    T rd[K];            // RN(1 / L[j][j]) for the columns with entries below the diagonal
 
     // _gather_joint! (src/kernels.jl:9-23). nbr is the int32 structure-of-arrays neighbour
     // table nbr[j*M + m]; coords is point-major.
@@ -383,12 +397,13 @@ struct Block {
             const bool ok = s > pivmin;  // false for NaN, as in the reference
             const T d = ok ? num<T>::sqrt(s) : dmin;
             A[tri(j, j)] = d;
+            if (j < K) rd[j] = T(1) / d;
 #pragma unroll
             for (int i = j + 1; i < N; ++i) {
                 T t = A[tri(i, j)];
 #pragma unroll
                 for (int p = 0; p < j; ++p) t = num<T>::fma(-A[tri(i, p)], A[tri(j, p)], t);
-                A[tri(i, j)] = ok ? t / d : T(0);
+                A[tri(i, j)] = ok ? div_rcp(t, d, rd[j]) : T(0);
             }
         }
     }
@@ -402,7 +417,7 @@ struct Block {
             T s = A[tri(K, i)];
 #pragma unroll
             for (int j = i + 1; j < K; ++j) s = num<T>::fma(-A[tri(j, i)], x[j], s);
-            x[i] = d > pivfloor ? s / d : T(0);
+            x[i] = d > pivfloor ? div_rcp(s, d, rd[i]) : T(0);
         }
     }
 

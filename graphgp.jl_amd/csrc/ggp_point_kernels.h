@@ -16,7 +16,8 @@
 //                     workgroup to a partials buffer (no global atomics)
 //
 // Layout in HBM: coords point-major uint32 (D per point); neighbours int32 SoA nbr[j*M + m];
-// mean_vec SoA mv[j*M + m]; std sd[m]; field arrays in tree order.
+// mean_vec point-major mv[m*k + j] (a consumer's k weights share a cache line: the reverse
+// sweep gathers them by list entry m*k + j); std sd[m]; field arrays in tree order.
 //
 // Included only by ggp_inst.hip, which is compiled once per (element type, k) so the heavy,
 // fully unrolled instantiations build in parallel; ggp_kernels.hip dispatches to them.
@@ -79,7 +80,7 @@ __device__ inline double factor_points(const uint32_t* __restrict__ coords,
             blk.mean_vec(x);
             if (MODE & F_MV) {
 #pragma unroll
-                for (int j = 0; j < K; ++j) mv[(int64_t)j * M + m] = x[j];
+                for (int j = 0; j < K; ++j) mv[m * K + j] = x[j];
                 sd[m] = s;
             }
             if (MODE & F_INV) {  // src/kernels.jl:48-55
@@ -220,7 +221,7 @@ k_sweep_fwd(T* __restrict__ v, const T* __restrict__ xi, int64_t xi_off,
                 for (int u = 0; u < B; ++u) {
                     live[u] = j0 + u < Krt;
                     q[u] = live[u] ? nbr[(int64_t)(j0 + u) * M + m] : 0;
-                    w[u] = live[u] ? mv[(int64_t)(j0 + u) * M + m] : T(0);
+                    w[u] = live[u] ? mv[m * Krt + j0 + u] : T(0);
                 }
                 sweep_read_all<T, B>(x, v, q, live, err);
 #pragma unroll
@@ -234,7 +235,7 @@ k_sweep_fwd(T* __restrict__ v, const T* __restrict__ xi, int64_t xi_off,
 #pragma unroll
             for (int j = 0; j < K; ++j) {
                 q[j] = nbr[(int64_t)j * M + m];
-                w[j] = mv[(int64_t)j * M + m];
+                w[j] = mv[m * K + j];
                 live[j] = true;
             }
             sweep_read_all<T, KA>(x, v, q, live, err);
@@ -294,7 +295,7 @@ k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
                 const uint32_t e = live[u] ? rev[(int64_t)ch.z + (int64_t)t * kBlock + tid] : 0u;
                 const uint32_t m = e / KK, j = e - m * KK;
                 p[u] = n0 + m;
-                w[u] = live[u] ? mv[(int64_t)j * M + m] : T(0);
+                w[u] = live[u] ? mv[(int64_t)m * KK + j] : T(0);
             }
             sweep_read_all<T, B>(x, vb, p, live, err);
             if (lg == 0) {

@@ -175,7 +175,7 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
         if (MODE & (F_MV | F_INV)) {
             const T xm = wide_mean_vec(a, K, lane);
             if (MODE & F_MV) {
-                if (lane < K) mv[(int64_t)lane * M + m] = xm;
+                if (lane < K) mv[m * K + lane] = xm;
                 if (lane == 0) sd[m] = s;
             }
             if (MODE & F_INV) {  // src/kernels.jl:48-55

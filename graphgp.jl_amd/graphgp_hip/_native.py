@@ -52,6 +52,8 @@ _HIP_SIGS = {
     "ggp_kernel_timers": (C.c_int, [_P, _I32]),
     "ggp_kernel_timer_read": (C.c_int, [_P, C.c_char_p, _DP, C.POINTER(_I64)]),
     "ggp_selftest_sqrt_f32": (C.c_int, [C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64)]),
+    "ggp_selftest_div": (C.c_int, [C.c_int32, C.c_uint64, C.c_uint64, C.c_uint32, C.c_uint64,
+                                   C.POINTER(C.c_uint64)]),
     "ggp_generate": (C.c_int, [_P, _P, _P, _P]),
     "ggp_generate_inv": (C.c_int, [_P, _P, _P, _P]),
     "ggp_generate_logdet": (C.c_int, [_P, _DP, _P]),

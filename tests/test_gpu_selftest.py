@@ -20,3 +20,25 @@ def test_lattice_sqrt_is_correctly_rounded(gpu, lo, hi):
     bad = C.c_uint64(0)
     nat.call("ggp_selftest_sqrt_f32", b0, b1 - b0 + 1, C.byref(bad))
     assert bad.value == 0
+
+
+@pytest.mark.parametrize("lo,hi", [(2.0 ** -20, 2.0 ** 0), (2.0 ** 0, 2.0 ** 20)])
+def test_cholesky_division_matches_ieee_f32(gpu, lo, hi):
+    """The per-point Cholesky and mean_vec divide by one reciprocal per column plus a one-fma
+    remainder correction; over every f32 divisor in [lo, hi) (the range of L[j][j] for tables of
+    moderate variance) with zero and 3 random numerators over 2^-100 .. 2^100 each, it must equal
+    the IEEE division bit for bit."""
+    from graphgp_hip import _native as nat
+    b0, b1 = _bits(lo), _bits(hi)
+    bad = C.c_uint64(0)
+    nat.call("ggp_selftest_div", 0, b0, b1 - b0, 4, 20261202, C.byref(bad))
+    assert bad.value == 0
+
+
+def test_cholesky_division_matches_ieee_f64(gpu):
+    """The same division in f64: 2^26 random divisors over 2^-60 .. 2^60, each with zero and 7
+    random numerators over 2^-900 .. 2^900."""
+    from graphgp_hip import _native as nat
+    bad = C.c_uint64(0)
+    nat.call("ggp_selftest_div", 1, 0, 1 << 26, 8, 7, C.byref(bad))
+    assert bad.value == 0
