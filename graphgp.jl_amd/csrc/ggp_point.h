@@ -425,18 +425,20 @@ struct Block {
 };
 
 // chol_pullback! (src/linalg.jl:112-137), under @fastmath. Lbar holds the factor cotangents on
-// entry and is consumed; Abar receives d/dA for the lower triangle.
+// entry and is consumed; Abar receives d/dA for the lower triangle. rd[j] = RN(1 / L[j][j]) for
+// j < N - 1 (Block::rd): the divisions by L[j][j] and 2 L[j][j] use it (div_rcp, the IEEE
+// quotient), the last column's one division is a plain division.
 template <typename T, int N>
 __device__ inline void chol_pullback(T (&Abar)[N * (N + 1) / 2], T (&Lbar)[N * (N + 1) / 2],
-                                     const T (&L)[N * (N + 1) / 2]) {
+                                     const T (&L)[N * (N + 1) / 2], const T (&rd)[N - 1]) {
 #pragma unroll
     for (int j = N - 1; j >= 0; --j) {
         const T ljj = L[tri(j, j)];
 #pragma unroll
         for (int i = N - 1; i >= j + 1; --i) {
             const T lbij = Lbar[tri(i, j)];
-            const T tbar = lbij / ljj;
-            Lbar[tri(j, j)] -= lbij * L[tri(i, j)] / ljj;
+            const T tbar = div_rcp(lbij, ljj, rd[j]);
+            Lbar[tri(j, j)] -= div_rcp(lbij * L[tri(i, j)], ljj, rd[j]);
             Abar[tri(i, j)] = tbar;
 #pragma unroll
             for (int p = 0; p < j; ++p) {
@@ -444,7 +446,8 @@ __device__ inline void chol_pullback(T (&Abar)[N * (N + 1) / 2], T (&Lbar)[N * (
                 Lbar[tri(j, p)] = num<T>::fma(-tbar, L[tri(i, p)], Lbar[tri(j, p)]);
             }
         }
-        const T sbar = Lbar[tri(j, j)] / (T(2) * ljj);
+        const T sbar = j < N - 1 ? div_rcp(Lbar[tri(j, j)], T(2) * ljj, rd[j < N - 1 ? j : 0] * T(0.5))
+                                 : Lbar[tri(j, j)] / (T(2) * ljj);
         Abar[tri(j, j)] = sbar;
 #pragma unroll
         for (int p = 0; p < j; ++p)

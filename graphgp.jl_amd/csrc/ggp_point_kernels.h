@@ -433,7 +433,7 @@ __device__ inline double pullback_points(const uint32_t* __restrict__ coords,
                     T t = zbar[i];
 #pragma unroll
                     for (int p = 0; p < i; ++p) t -= blk.A[tri(i, p)] * zbar[p];
-                    zbar[i] = t / blk.A[tri(i, i)];
+                    zbar[i] = div_rcp(t, blk.A[tri(i, i)], blk.rd[i]);
                 }
             } else {
                 // src/kernels_adjoint.jl:509-538: seeds from vb[p], xi[p], v[neighbours], with
@@ -448,7 +448,7 @@ __device__ inline double pullback_points(const uint32_t* __restrict__ coords,
                     T t = zbar[i];
 #pragma unroll
                     for (int p = 0; p < i; ++p) t -= blk.A[tri(i, p)] * zbar[p];
-                    zbar[i] = blk.A[tri(i, i)] > pivfloor ? t / blk.A[tri(i, i)] : T(0);
+                    zbar[i] = blk.A[tri(i, i)] > pivfloor ? div_rcp(t, blk.A[tri(i, i)], blk.rd[i]) : T(0);
                 }
             }
 #pragma unroll
@@ -458,7 +458,7 @@ __device__ inline double pullback_points(const uint32_t* __restrict__ coords,
                 for (int i = 0; i <= j; ++i) Lbar[tri(j, i)] -= zbar[i] * x[j];
             }
         }
-        chol_pullback<T, N>(Abar, Lbar, blk.A);
+        chol_pullback<T, N>(Abar, Lbar, blk.A, blk.rd);
         if (PTS)
             scatter_pts<T, K, D, ONE>(hist_partial, blk, nb, m, n0, Abar, scale, s_tab, s_acc, P);
         else
