@@ -309,60 +309,68 @@ constexpr int kLtPitch = kTile + 4;  // transposed L rows, 16-byte aligned
 __host__ __device__ inline int dense_sync_flag_ints(int nt) { return (nt * nt + 2 * nt + 2) & ~1; }
 
 // Walker factor of the tile in sA into global tile (j, j) and, transposed, into Lt (LDS; zero
-// above the diagonal). Right-looking by columns: lane r owns row r; at step p the pivot and the
-// column values come from their lanes by readlane, and every entry (r, c), c > p, takes
-// fma(-L[r][p], L[c][p], .). Entries above the diagonal are scratch (updated, never stored).
-// f64: L[p][p] = sqrt(pivot) and the column divided by it, the unblocked left-looking chain in
-// its order (the oracle's bits). f32: one reciprocal square root per column (v_rsq_f32, within
-// 1 ulp): L[p][p] = pivot * rsq and the column multiplied by rsq, which takes the square root
-// and the division off the column-to-column chain; rsq goes to inv (LDS) and dinv (global, for
-// the helpers' solves). Called by wave 0.
+// above the diagonal). Right-looking by columns on one wavefront: lane 32h + r holds row r,
+// columns 16h .. 16h+15. At step p the pivot comes from its lane by readlane; the lanes holding
+// column p scale it and publish it to LDS (col, rows <= p as zero), and every lane reads its 16
+// column values back with broadcast reads and updates all 16 of its entries: entry (r, c) takes
+// fma(-L[r][p], L[c][p], .) when p < c, and fma(-L[r][p], 0, .) (no change) otherwise, so each
+// entry keeps the unblocked left-looking chain in its order. Entries above the diagonal are
+// scratch (updated, never stored).
+// f64: L[p][p] = sqrt(pivot) and the column divided by it (the oracle's bits). f32: one
+// reciprocal square root per column (v_rsq_f32, within 1 ulp): L[p][p] = pivot * rsq and the
+// column multiplied by rsq, which takes the square root and the division off the
+// column-to-column chain; rsq goes to inv (LDS) and dinv (global, for the helpers' solves).
+// Called by wave 0.
 template <typename T>
 __device__ inline void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1],
-                                     T (*Lt)[kLtPitch], T* inv, T* dinv, int tid, int* info) {
+                                     T (*Lt)[kLtPitch], T* inv, T* dinv, T (*col)[kTile],
+                                     int tid, int* info) {
     constexpr bool kRsq = std::is_same<T, float>::value;
-    const int r = tid & (kTile - 1);
-    const bool live = tid < kTile && j * kTile + r < n;
-    T a[kTile];
+    const int r = tid & (kTile - 1), h = tid >> 5;
+    const bool live = j * kTile + r < n;
+    T a[16];
 #pragma unroll
-    for (int cc = 0; cc < kTile; ++cc) a[cc] = sA[r][cc];
+    for (int u = 0; u < 16; ++u) a[u] = sA[r][16 * h + u];
     bool bad = false;
     T myinv = T(0);
 #pragma unroll
     for (int p = 0; p < kTile; ++p) {
-        const T piv = bcast(a[p], p);
+        const int hp = p >> 4, up = p & 15;
+        const bool mine = h == hp;  // this lane holds column p
+        const T piv = bcast(a[up], 32 * hp + p);
         bad = bad || !(piv > T(0));
         T d, l;
         if (kRsq) {
             const T rs = (T)__builtin_amdgcn_rsqf((float)piv);
             d = piv * rs;
-            l = a[p] * rs;
-            myinv = r == p ? rs : myinv;
+            l = a[up] * rs;
+            myinv = (mine && r == p) ? rs : myinv;
         } else {
             d = num<T>::sqrt(piv);
-            l = a[p] / d;
+            l = a[up] / d;
         }
-        a[p] = r == p ? d : l;
-        // column p from its lanes first (separate scalars: no read-after-readlane stall per
-        // entry), then the updates
-        T col[kTile];
+        a[up] = mine ? (r == p ? d : l) : a[up];
+        T* cp = col[p & 1];
+        if (mine) cp[r] = r > p ? l : T(0);
+        wave_sync_lds();
+        const T own = cp[r];
+        T cv[16];
 #pragma unroll
-        for (int cc = p + 1; cc < kTile; ++cc) col[cc] = bcast(a[p], cc);
+        for (int u = 0; u < 16; ++u) cv[u] = cp[16 * h + u];
 #pragma unroll
-        for (int cc = p + 1; cc < kTile; ++cc) a[cc] = num<T>::fma(-a[p], col[cc], a[cc]);
+        for (int u = 0; u < 16; ++u) a[u] = num<T>::fma(-own, cv[u], a[u]);
     }
+    const bool diag_lane = h == (r >> 4);  // holds L[r][r] (and its reciprocal)
     if (live) {
-        T* wp = A + (int64_t)(j * kTile + r) * n + j * kTile;
+        T* wp = A + (int64_t)(j * kTile + r) * n + j * kTile + 16 * h;
 #pragma unroll
-        for (int cc = 0; cc < kTile; ++cc)
-            if (cc <= r) wp[cc] = a[cc];
-        if (kRsq) dinv[j * kTile + r] = myinv;
+        for (int u = 0; u < 16; ++u)
+            if (16 * h + u <= r) wp[u] = a[u];
+        if (kRsq && diag_lane) dinv[j * kTile + r] = myinv;
     }
-    if (tid < kTile) {
-        if (kRsq) inv[r] = myinv;
+    if (kRsq && diag_lane) inv[r] = myinv;
 #pragma unroll
-        for (int cc = 0; cc < kTile; ++cc) Lt[cc][r] = cc <= r ? a[cc] : T(0);
-    }
+    for (int u = 0; u < 16; ++u) Lt[16 * h + u][r] = 16 * h + u <= r ? a[u] : T(0);
     if (tid == 0 && bad) atomicOr(info, 1);
 }
 
@@ -431,6 +439,7 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, in
     __shared__ T sP[kTile][kTile + 1];            // walker: L[j][j-1], then L[j+1][j]
     __shared__ __align__(16) T sLt[kTile][kLtPitch];  // walker: L[j][j] transposed
     __shared__ T sInv[kTile];                         // f32: 1 / L[p][p] of the current tile
+    __shared__ __align__(16) T sCol[2][kTile];        // walker factor: the published column
     __shared__ int s_task;
     int* ticket = sync;
     int* flags = sync + 1;
@@ -469,7 +478,7 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, in
             for (int q = 0; q < 4; ++q) sA[r0 + 8 * q][c] = acc[q];
             __syncthreads();
             if (w == 0) {
-                walk_factor_t(A, n, j, sA, sLt, sInv, dinv, tid, info);
+                walk_factor_t(A, n, j, sA, sLt, sInv, dinv, sCol, tid, info);
             } else if (sub && w <= 2) {
                 // sub-diagonal tile: partial sum over k < j-1 plus the k = j-1 term, into sC
                 const int R = 16 * (w - 1);
