@@ -315,7 +315,13 @@ int finish(ggp_graph* h, hipStream_t user) {
     tstop(h, TM_OP, h->s_main);
     HC(hipEventRecord(h->ev_user, h->s_main));
     HC(hipStreamWaitEvent(user, h->ev_user, 0));
-    HC(hipStreamSynchronize(h->s_main));
+    // Poll the op's last event rather than block in hipStreamSynchronize: a blocking wait
+    // returns to the host tens of microseconds after the stream drains, a poll within one or two.
+    for (;;) {
+        const hipError_t q = hipEventQuery(h->ev_user);
+        if (q == hipSuccess) break;
+        if (q != hipErrorNotReady) return fail(GGP_ERR_HIP, std::string("op: ") + hipGetErrorString(q));
+    }
     tcollect(h);
     if (h->herr[0] & 4) {
         h->herr[0] = 0;

@@ -250,11 +250,16 @@ def _empty(n, dtype):
 
 
 def _stream():
-    return C.c_void_p(_torch().cuda.current_stream().cuda_stream)
+    torch = _torch()
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)  # ~0.1 us against ~3 us
+    if raw is not None:
+        return C.c_void_p(raw(torch.cuda.current_device()))
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
 def _out(t, n, as_numpy):
-    t = t[:n]
+    if t.numel() != n:
+        t = t[:n]
     return t.cpu().numpy() if as_numpy else t
 
 
