@@ -424,11 +424,11 @@ int check_ready(ggp_graph* h) {
 // xi[xi_off + m].
 template <typename T>
 void sweep_forward(ggp_graph* h, T* v, const T* xi, int64_t xi_off, hipStream_t st,
-                   bool prepared = false) {
+                   bool prepared = false, T* out = nullptr, const int32_t* oidx = nullptr) {
     const Graph& g = h->g;
     tstart(h, TM_SWEEP_FWD, st);
     launch_sweep_fwd<T>(g, v, xi, xi_off, tp<T>(h->mv), tp<T>(h->sd),
-                        table<T>(h).aniso.grid != nullptr, prepared, st);
+                        table<T>(h).aniso.grid != nullptr, prepared, st, out, oidx);
     tstop(h, TM_SWEEP_FWD, st);
 }
 
@@ -436,11 +436,22 @@ void sweep_forward(ggp_graph* h, T* v, const T* xi, int64_t xi_off, hipStream_t 
 // launch.
 template <typename T>
 void sweep_reverse(ggp_graph* h, T* vb, const T* vbar, T* xg, hipStream_t st,
-                   bool prepared = false) {
+                   bool prepared = false, T* xout = nullptr, const int32_t* oidx = nullptr) {
     const Graph& g = h->g;
     tstart(h, TM_SWEEP_REV, st);
-    launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), prepared, st);
+    launch_sweep_rev<T>(g, vb, vbar, xg, tp<T>(h->mv), tp<T>(h->sd), prepared, st, xout, oidx);
     tstop(h, TM_SWEEP_REV, st);
+}
+
+// out[idx[i]] = x[i] for the positions past the last level (the products and sweeps store the
+// rest of an op's original-order output themselves).
+template <typename T>
+void scatter_tail(ggp_graph* h, T* out, const T* x, hipStream_t st) {
+    const Graph& g = h->g;
+    const int64_t end = g.offsets.back();
+    if (end >= g.N) return;
+    if (g.idx) launch_scatter<T>(out, x + end, g.idx + end, g.N - end, st);
+    else launch_scatter<T>(out + end, x + end, (const int32_t*)nullptr, g.N - end, st);  // identity
 }
 
 // Points past the last level are never refined by the reference (values stay zero).
@@ -466,9 +477,10 @@ int op_generate(ggp_graph* h, const T* xi, T* out, hipStream_t user) {
     zero_tail<T>(h, v, h->s_main);
     factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr, nullptr);
     if (int rc = join(h)) return rc;
-    dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_main);
-    sweep_forward<T>(h, v, xt, g.n0, h->s_main, true);
-    launch_scatter<T>(out, v, g.idx, g.N, h->s_main);
+    // L xi and the sweep also store their values at out[idx[i]] (original order)
+    dense_trmv<T>(tp<T>(h->A), (int)g.n0, xt, v, h->s_main, out, g.idx);
+    sweep_forward<T>(h, v, xt, g.n0, h->s_main, true, out, g.idx);
+    scatter_tail<T>(h, out, v, h->s_main);
     if (int rc = finish(h, user)) return rc;
     if (*h->hinfo != 0) {
         if (int rc = dense_retry<T>(h)) return rc;
@@ -600,10 +612,11 @@ int op_grad_xi(ggp_graph* h, const T* vbar, T* xbar, hipStream_t user) {
     zero_tail<T>(h, xg, h->s_main);
     factor_t<T>(h, F_MV, tp<T>(h->mv), tp<T>(h->sd), nullptr, nullptr, nullptr,
                      nullptr);
-    sweep_reverse<T>(h, vb, vbt, xg, h->s_main, true);
+    // the sweep and L^T vb also store their values at xbar[idx[i]] (original order)
+    sweep_reverse<T>(h, vb, vbt, xg, h->s_main, true, xbar, g.idx);
     if (int rc = join(h)) return rc;
-    dense_trmv_t<T>(tp<T>(h->A), (int)g.n0, vb, xg, h->s_main);
-    launch_scatter<T>(xbar, xg, g.idx, g.N, h->s_main);
+    dense_trmv_t<T>(tp<T>(h->A), (int)g.n0, vb, xg, h->s_main, xbar, g.idx);
+    scatter_tail<T>(h, xbar, xg, h->s_main);
     if (int rc = finish(h, user)) return rc;
     if (*h->hinfo != 0) {
         if (int rc = dense_retry<T>(h)) return rc;

@@ -641,7 +641,8 @@ __device__ inline Acc tv_chain(const T* __restrict__ row, const T* __restrict__ 
 // y = L x (src/dense.jl:118): row i accumulates j = 0..i.
 template <typename T, typename Acc, typename Out>
 __global__ void __launch_bounds__(256) k_trmv(const T* __restrict__ L, int n,
-                                              const T* __restrict__ x, Out* __restrict__ y) {
+                                              const T* __restrict__ x, Out* __restrict__ y,
+                                              Out* __restrict__ out, const int32_t* __restrict__ oidx) {
     constexpr int pitch = kTvCols + 16 / (int)sizeof(T);
     __shared__ __align__(16) T sL[kTvRows * pitch];
     __shared__ __align__(16) T sx[kTvCols];
@@ -667,12 +668,16 @@ __global__ void __launch_bounds__(256) k_trmv(const T* __restrict__ L, int n,
         if (tid < nr)
             acc = tv_chain<T, Acc>(sL + tid * pitch, sx, 0, min(i0 + tid + 1, j0 + w) - j0, acc);
     }
-    if (tid < nr) y[i0 + tid] = (Out)acc;
+    if (tid < nr) {
+        y[i0 + tid] = (Out)acc;
+        if (out) out[oidx ? oidx[i0 + tid] : i0 + tid] = (Out)acc;  // null map: identity
+    }
 }
 // y = L^T x (src/grad.jl:457, 493): entry i accumulates j = i..n-1.
 template <typename T, typename Acc, typename Out>
 __global__ void __launch_bounds__(256) k_trmv_t(const T* __restrict__ L, int n,
-                                                const T* __restrict__ x, Out* __restrict__ y) {
+                                                const T* __restrict__ x, Out* __restrict__ y,
+                                                Out* __restrict__ out, const int32_t* __restrict__ oidx) {
     constexpr int pitch = kTvCols + 16 / (int)sizeof(T);
     __shared__ __align__(16) T sL[kTvRows * pitch];
     __shared__ __align__(16) T sx[kTvCols];
@@ -698,7 +703,10 @@ __global__ void __launch_bounds__(256) k_trmv_t(const T* __restrict__ L, int n,
         if (tid < nr)
             acc = tv_chain<T, Acc>(sL + tid * pitch, sx, max(i0 + tid - j0, 0), w, acc);
     }
-    if (tid < nr) y[i0 + tid] = (Out)acc;
+    if (tid < nr) {
+        y[i0 + tid] = (Out)acc;
+        if (out) out[oidx ? oidx[i0 + tid] : i0 + tid] = (Out)acc;  // null map: identity
+    }
 }
 
 // x = L \ b (src/dense.jl:134), one workgroup: 32-row diagonal blocks solved by wave 0 with
@@ -778,12 +786,15 @@ __global__ void k_logdiag(const T* __restrict__ L, int n, double* __restrict__ o
 }
 
 template <typename T>
-void dense_trmv(const T* L, int n, const T* x, T* y, hipStream_t st) {
-    hipLaunchKernelGGL((k_trmv<T, T, T>), dim3(cdiv(n, kTvRows)), dim3(256), 0, st, L, n, x, y);
+void dense_trmv(const T* L, int n, const T* x, T* y, hipStream_t st, T* out, const int32_t* oidx) {
+    hipLaunchKernelGGL((k_trmv<T, T, T>), dim3(cdiv(n, kTvRows)), dim3(256), 0, st, L, n, x, y,
+                       out, oidx);
 }
 template <typename T>
-void dense_trmv_t(const T* L, int n, const T* x, T* y, hipStream_t st) {
-    hipLaunchKernelGGL((k_trmv_t<T, T, T>), dim3(cdiv(n, kTvRows)), dim3(256), 0, st, L, n, x, y);
+void dense_trmv_t(const T* L, int n, const T* x, T* y, hipStream_t st, T* out,
+                  const int32_t* oidx) {
+    hipLaunchKernelGGL((k_trmv_t<T, T, T>), dim3(cdiv(n, kTvRows)), dim3(256), 0, st, L, n, x, y,
+                       out, oidx);
 }
 template <typename T>
 void dense_trsv(const T* L, int n, const T* b, T* x, hipStream_t st) {
@@ -1167,7 +1178,7 @@ void dense_grad_generate(const Graph& g, const Table<T>& tb, const T* L, const T
     if (!inverse_ready) dense_inverse64(L, n, W, C, st);
     // u = L^T vb in double (rows i >= a, increasing i)
     hipLaunchKernelGGL((k_trmv_t<T, double, double>), dim3(cdiv(n, kTvRows)), dim3(256), 0, st, L,
-                       n, vb, u);
+                       n, vb, u, (double*)nullptr, (const int32_t*)nullptr);
     hipLaunchKernelGGL((k_qprefix<T>), dim3(cdiv(n, 32)), dim3(256), 0, st, W, n, xi, u, Q);
     launch_gemm<double>({gemm_job(W, n, 1, Q, n, C, n, n, n, n, GK_FROM_I | GK_FROM_J, 1.0)}, st);
     launch_dense_scatter<T, DM_GENERATE>(g, tb, C, nullptr, hist_partial, nw, st);
@@ -1264,8 +1275,9 @@ void dense_grad_points_invloss(const Graph& g, const Table<T>& tb, const T* alph
     template void dense_assemble<T>(const Graph&, const Table<T>&, T*, T, hipStream_t, int*,   \
                                     int*);                                                     \
     template void dense_potrf<T>(T*, int, int*, int*, int, hipStream_t, bool);                            \
-    template void dense_trmv<T>(const T*, int, const T*, T*, hipStream_t);                     \
-    template void dense_trmv_t<T>(const T*, int, const T*, T*, hipStream_t);                   \
+    template void dense_trmv<T>(const T*, int, const T*, T*, hipStream_t, T*, const int32_t*); \
+    template void dense_trmv_t<T>(const T*, int, const T*, T*, hipStream_t, T*,                \
+                                  const int32_t*);                                             \
     template void dense_trsv<T>(const T*, int, const T*, T*, hipStream_t);                     \
     template void dense_trsv_t<T>(const T*, int, const T*, T*, hipStream_t);                   \
     template void dense_logdiag<T>(const T*, int, double*, hipStream_t);                       \

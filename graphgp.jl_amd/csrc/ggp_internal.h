@@ -77,9 +77,10 @@ struct PointK {
                          const T* vb, double* hist_partial, double* scalar_partial,
                          unsigned nblk, hipStream_t st);
     static void sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                          const T* sd, bool two_pass, hipStream_t st);
-    static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
+                          const T* sd, bool two_pass, T* out, const int32_t* oidx,
                           hipStream_t st);
+    static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
+                          T* xout, const int32_t* oidx, hipStream_t st);
 };
 // The same launchers for any k <= 31 (wavefront-per-point kernels, ggp_wide.h).
 template <typename T>
@@ -91,9 +92,10 @@ struct WideK {
                          const T* vb, double* hist_partial, double* scalar_partial,
                          unsigned nblk, hipStream_t st);
     static void sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                          const T* sd, bool two_pass, hipStream_t st);
-    static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
+                          const T* sd, bool two_pass, T* out, const int32_t* oidx,
                           hipStream_t st);
+    static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
+                          T* xout, const int32_t* oidx, hipStream_t st);
 };
 extern template struct WideK<float>;
 extern template struct WideK<double>;
@@ -136,14 +138,19 @@ void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, c
 // Whole sweeps, one launch each: the forward apply over every level (v[n0:end] is written) and
 // the reverse gather (vb and xg of every position in a level or the dense block).
 // prepared: launch_sweep_prep already ran for this sweep (else the sweep prepares itself).
+// out / xout (optional): every value the sweep produces (v, or xg = std * vb) is also stored at
+// out[oidx[position]] (the op's original-order output, so no separate scatter is needed); a null
+// oidx is the identity map, as in launch_scatter.
 template <typename T>
 void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                      const T* sd, bool two_pass, bool prepared, hipStream_t st);
+                      const T* sd, bool two_pass, bool prepared, hipStream_t st,
+                      T* out = nullptr, const int32_t* oidx = nullptr);
 template <typename T>
 void launch_sumsq_half(const T* x, int64_t n, double* out, hipStream_t st);
 template <typename T>
 void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                      bool prepared, hipStream_t st);
+                      bool prepared, hipStream_t st, T* xout = nullptr,
+                      const int32_t* oidx = nullptr);
 // Pending markers for the next forward (v) and/or reverse (vb) sweep, tickets zeroed.
 template <typename T>
 void launch_sweep_prep(const Graph& g, T* v, T* vb, hipStream_t st);
@@ -189,10 +196,13 @@ template <typename T>
 void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st,
                  bool zeroed = false);
 int dense_sync_ints(int n);
+// y = L x and y = L^T x; out (optional): y[i] also stored at out[oidx[i]] (null oidx: out[i]).
 template <typename T>
-void dense_trmv(const T* L, int n, const T* x, T* y, hipStream_t st);
+void dense_trmv(const T* L, int n, const T* x, T* y, hipStream_t st, T* out = nullptr,
+                const int32_t* oidx = nullptr);
 template <typename T>
-void dense_trmv_t(const T* L, int n, const T* x, T* y, hipStream_t st);
+void dense_trmv_t(const T* L, int n, const T* x, T* y, hipStream_t st, T* out = nullptr,
+                  const int32_t* oidx = nullptr);
 template <typename T>
 void dense_trsv(const T* L, int n, const T* b, T* x, hipStream_t st);
 template <typename T>

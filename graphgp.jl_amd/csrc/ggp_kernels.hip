@@ -112,14 +112,15 @@ void WideK<T>::pullback(const Graph& g, const Table<T>& tb, int mode, const T* v
 
 template <typename T>
 void WideK<T>::sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                         const T* sd, bool two_pass, hipStream_t st) {
-    PointK<T, 0>::sweep_fwd(g, v, xi, xi_off, mv, sd, two_pass, st);
+                         const T* sd, bool two_pass, T* out, const int32_t* oidx,
+                         hipStream_t st) {
+    PointK<T, 0>::sweep_fwd(g, v, xi, xi_off, mv, sd, two_pass, out, oidx, st);
 }
 
 template <typename T>
 void WideK<T>::sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                         hipStream_t st) {
-    PointK<T, 0>::sweep_rev(g, vb, vbar, xg, mv, sd, st);
+                         T* xout, const int32_t* oidx, hipStream_t st) {
+    PointK<T, 0>::sweep_rev(g, vb, vbar, xg, mv, sd, xout, oidx, st);
 }
 
 template struct WideK<float>;
@@ -187,20 +188,21 @@ void launch_sweep_prep(const Graph& g, T* v, T* vb, hipStream_t st) {
 
 template <typename T>
 void launch_sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                      const T* sd, bool two_pass, bool prepared, hipStream_t st) {
+                      const T* sd, bool two_pass, bool prepared, hipStream_t st, T* out,
+                      const int32_t* oidx) {
     if (g.n_fwd_chunks == 0) return;
     if (!prepared) launch_sweep_prep<T>(g, v, (T*)nullptr, st);
-#define CALLS(KK) Launch<T, KK>::sweep_fwd(g, v, xi, xi_off, mv, sd, two_pass, st)
+#define CALLS(KK) Launch<T, KK>::sweep_fwd(g, v, xi, xi_off, mv, sd, two_pass, out, oidx, st)
     GGP_FOR_K(CALLS);
 #undef CALLS
 }
 
 template <typename T>
 void launch_sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
-                      bool prepared, hipStream_t st) {
+                      bool prepared, hipStream_t st, T* xout, const int32_t* oidx) {
     if (g.n_rev_chunks == 0) return;
     if (!prepared) launch_sweep_prep<T>(g, (T*)nullptr, vb, st);
-#define CALLR(KK) Launch<T, KK>::sweep_rev(g, vb, vbar, xg, mv, sd, st)
+#define CALLR(KK) Launch<T, KK>::sweep_rev(g, vb, vbar, xg, mv, sd, xout, oidx, st)
     GGP_FOR_K(CALLR);
 #undef CALLR
 }
@@ -336,9 +338,9 @@ void launch_sqrt_check(uint32_t b0, uint32_t count, unsigned long long* bad, hip
     template void launch_pullback<T>(const Graph&, const Table<T>&, int, const T*, const T*,   \
                                      const T*, double*, double*, unsigned, hipStream_t);       \
     template void launch_sweep_fwd<T>(const Graph&, T*, const T*, int64_t, const T*, const T*, \
-                                      bool, bool, hipStream_t);                                \
+                                      bool, bool, hipStream_t, T*, const int32_t*);            \
     template void launch_sweep_rev<T>(const Graph&, T*, const T*, T*, const T*, const T*,      \
-                                      bool, hipStream_t);                                      \
+                                      bool, hipStream_t, T*, const int32_t*);                  \
     template void launch_sweep_prep<T>(const Graph&, T*, T*, hipStream_t);                     \
     template void launch_fill_pending<T>(T*, int64_t, hipStream_t);                            \
     template void launch_reduce_hist<T>(T*, const double*, int, int, const double*,            \

@@ -202,7 +202,8 @@ __global__ void __launch_bounds__(kBlock)
 k_sweep_fwd(T* __restrict__ v, const T* __restrict__ xi, int64_t xi_off,
             const T* __restrict__ mv, const T* __restrict__ sd, const int32_t* __restrict__ nbr,
             int64_t M, int64_t n0, int Krt, const int4* __restrict__ chunks, int nchunks,
-            int* __restrict__ ticket, int* __restrict__ err) {
+            int* __restrict__ ticket, int* __restrict__ err, T* __restrict__ out,
+            const int32_t* __restrict__ oidx) {
     __shared__ int s_c;
     constexpr int KA = K > 0 ? K : 1;
     for (int c = sweep_next(ticket, &s_c); c < nchunks; c = sweep_next(ticket, &s_c)) {
@@ -244,6 +245,7 @@ k_sweep_fwd(T* __restrict__ v, const T* __restrict__ xi, int64_t xi_off,
         }
         if (TWO_PASS) acc = acc + s_xi;
         sweep_publish(v + n0 + m, acc);
+        if (out) out[oidx ? (int64_t)oidx[n0 + m] : n0 + m] = acc;  // null map: identity
     }
 }
 
@@ -264,7 +266,7 @@ k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
             const T* __restrict__ mv, const T* __restrict__ sd, const uint32_t* __restrict__ rcnt,
             const uint32_t* __restrict__ rev, int64_t M, int64_t n0, int Krt,
             const int4* __restrict__ chunks, int nchunks, int* __restrict__ ticket,
-            int* __restrict__ err) {
+            int* __restrict__ err, T* __restrict__ xout, const int32_t* __restrict__ oidx) {
     constexpr int B = kRevSlots;
     __shared__ int s_c;
     __shared__ T s_prod[B][kBlock];
@@ -284,6 +286,8 @@ k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
         const int64_t q = (int64_t)ch.x + i;
         const int cnt = pt ? (int)rcnt[q] : 0;
         T acc = (pt && sub == 0) ? vbar[q] : T(0);
+        // std of the point, fetched with the list counts (off the chunk's tail)
+        const T sdq = (xg && pt && sub == 0 && q >= n0) ? sd[q - n0] : T(0);
         for (int t0 = 0; t0 < nslots; t0 += B) {
             int64_t p[B];
             bool live[B];
@@ -317,7 +321,11 @@ k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
         }
         if (pt && sub == 0) {
             sweep_publish(vb + q, acc);
-            if (xg && q >= n0) xg[q] = sd[q - n0] * acc;
+            if (xg && q >= n0) {
+                const T x = sdq * acc;
+                xg[q] = x;
+                if (xout) xout[oidx ? (int64_t)oidx[q] : q] = x;  // null map: identity
+            }
         }
         if (tid == 0) s_c = next;
         __syncthreads();
@@ -574,25 +582,26 @@ void PointK<T, K>::pullback(const Graph& g, const Table<T>& tb, int mode, const 
 
 template <typename T, int K>
 void PointK<T, K>::sweep_fwd(const Graph& g, T* v, const T* xi, int64_t xi_off, const T* mv,
-                             const T* sd, bool two_pass, hipStream_t st) {
+                             const T* sd, bool two_pass, T* out, const int32_t* oidx,
+                             hipStream_t st) {
     const unsigned nwg = (unsigned)std::max(1, std::min(g.n_fwd_chunks, g.sweep_wgs));
     if (two_pass)
         hipLaunchKernelGGL((k_sweep_fwd<T, K, true>), dim3(nwg), dim3(kBlock), 0, st, v, xi,
                            xi_off, mv, sd, g.nbr, g.M, g.n0, (int)g.K, g.fwd_chunks,
-                           g.n_fwd_chunks, g.sweep_ticket, g.sweep_err);
+                           g.n_fwd_chunks, g.sweep_ticket, g.sweep_err, out, oidx);
     else
         hipLaunchKernelGGL((k_sweep_fwd<T, K, false>), dim3(nwg), dim3(kBlock), 0, st, v, xi,
                            xi_off, mv, sd, g.nbr, g.M, g.n0, (int)g.K, g.fwd_chunks,
-                           g.n_fwd_chunks, g.sweep_ticket, g.sweep_err);
+                           g.n_fwd_chunks, g.sweep_ticket, g.sweep_err, out, oidx);
 }
 
 template <typename T, int K>
 void PointK<T, K>::sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv,
-                             const T* sd, hipStream_t st) {
+                             const T* sd, T* xout, const int32_t* oidx, hipStream_t st) {
     const unsigned nwg = (unsigned)std::max(1, std::min(g.n_rev_chunks, g.sweep_wgs));
     hipLaunchKernelGGL((k_sweep_rev<T, K>), dim3(nwg), dim3(kBlock), 0, st, vb, vbar, xg, mv, sd,
                        g.rcnt, g.rev, g.M, g.n0, (int)g.K, g.rev_chunks, g.n_rev_chunks,
-                       g.sweep_ticket + 1, g.sweep_err);
+                       g.sweep_ticket + 1, g.sweep_err, xout, oidx);
 }
 
 }  // namespace ggp
