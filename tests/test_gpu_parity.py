@@ -270,6 +270,30 @@ def test_dense_only_and_empty_levels(gpu, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+def test_refined_graph_without_permutation(gpu, dtype, monkeypatch):
+    """A refined graph with no permutation at all (no caller indices, and the library's internal
+    level order switched off with GGP_TREE_ORDER when the handle is made): the sweeps and the
+    triangular products then store the original-order outputs through the identity map."""
+    _say(f"case no_permutation {np.dtype(dtype).name}")
+    prob, _ = synth_problem(3000, 3, 120, 8, dtype, seed=11)
+    p2 = G().GraphGPProblem(prob.coords, prob.neighbors, prob.offsets, prob.n0, prob.scale,
+                            prob.bins, prob.vals)
+    r2 = O().Problem(p2.coords, p2.neighbors, p2.offsets, p2.n0, p2.scale, p2.bins, p2.vals,
+                     dtype=dtype)
+    monkeypatch.setenv("GGP_TREE_ORDER", "1")
+    hp = G().to_backend(p2)
+    monkeypatch.delenv("GGP_TREE_ORDER")
+    rng = np.random.default_rng(3)
+    xi = rng.standard_normal(p2.N).astype(dtype)
+    vb = rng.standard_normal(p2.N).astype(dtype)
+    t = tol(dtype)
+    assert relerr(G().generate(hp, xi), r2.generate(xi)) < t
+    assert relerr(G().generate_grad_xi(hp, vb), r2.generate_grad_xi(vb)) < t
+    assert relerr(G().generate_grad_vals(hp, xi, vb), r2.generate_grad_vals(xi, vb)) < (
+        t if dtype == np.float32 else 1e-10)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_dense_jitter_retry(gpu, dtype):
     """Coincident points make the dense block singular: the factorization is retried with
     escalating jitter (src/dense.jl:46-67, test/test_dense.jl:54-62)."""
