@@ -13,7 +13,11 @@ matrix); the forward values use the lattice coordinates and ignore it (straight-
 src/chainrules.jl:84-122).
 
 `vals` is a torch tensor (any device); setting it replaces the problem's table, as _set_vals
-does. d/d(data) of the inverse loss is not provided, as in the reference (@not_implemented).
+does. The reference's pullbacks close over the problem their forward ran on (prob2 =
+_set_vals(prob, vals), src/chainrules.jl:32-37, src/grad_generate_vals.jl:294-305); here the
+handle is shared, so each Function records the table of its forward and puts it back before its
+pullback runs if another table was set in between. d/d(data) of the inverse loss is not
+provided, as in the reference (@not_implemented).
 """
 from __future__ import annotations
 
@@ -35,10 +39,12 @@ class _Generate(torch.autograd.Function):
     @staticmethod
     def forward(ctx, xi, prob):
         ctx.prob = prob
+        ctx.table = prob.table_snapshot()
         return P.generate(prob, xi)
 
     @staticmethod
     def backward(ctx, ybar):
+        ctx.prob.use_table(ctx.table)
         return P.generate_grad_xi(ctx.prob, ybar.contiguous()), None
 
 
@@ -75,6 +81,7 @@ class _GenerateOfVals(torch.autograd.Function):
     def forward(ctx, vals, xi, prob):
         _set(prob, vals)
         ctx.prob = prob
+        ctx.table = prob.table_snapshot()
         ctx.save_for_backward(xi)
         ctx.vals_meta = (vals.dtype, vals.device)
         return P.generate(prob, xi)
@@ -82,6 +89,7 @@ class _GenerateOfVals(torch.autograd.Function):
     @staticmethod
     def backward(ctx, ybar):
         (xi,) = ctx.saved_tensors
+        ctx.prob.use_table(ctx.table)
         yb = ybar.contiguous()
         dvals = P.generate_grad_vals(ctx.prob, xi, yb)
         dxi = P.generate_grad_xi(ctx.prob, yb)

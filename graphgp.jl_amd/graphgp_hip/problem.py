@@ -150,6 +150,8 @@ class HipProblem:
         self.N, self.n0, self.K, self.D, self.M = prob.N, prob.n0, prob.K, prob.D, prob.M
         self.dtype = prob.dtype
         self._h = C.c_void_p()
+        self.table_version = 0  # bumped by every set_vals / set_aniso
+        self._table = None
         idx = prob.indices
         nat.call("ggp_graph_create", C.byref(self._h), prob.coords.ctypes.data,
                  prob.neighbors.ctypes.data if prob.M else None, prob.offsets.ctypes.data,
@@ -170,14 +172,33 @@ class HipProblem:
         self.bins = self.vals = None
         nat.call("ggp_set_cov_aniso", self._h, sb.ctypes.data, len(sb), zb.ctypes.data, len(zb),
                  g.ctypes.data, float(cov.alpha))
+        self.table_version += 1
+        self._table = ("aniso", cov)
         return self
 
     def set_vals(self, vals, bins=None):
         """Replace the covariance table (the analogue of _set_vals, src/chainrules.jl:18-21)."""
         bins = self.host.bins if bins is None else np.ascontiguousarray(bins, dtype=self.dtype)
-        vals = _to_host(vals, self.dtype)
+        vals = _to_host(vals, self.dtype).copy()
         self.bins, self.vals = bins, vals
         nat.call("ggp_set_cov_iso", self._h, bins.ctypes.data, vals.ctypes.data, len(bins))
+        self.table_version += 1
+        self._table = ("iso", bins, vals)
+        return self
+
+    def table_snapshot(self):
+        """The covariance table in use now, for use_table(): a pullback closes over the problem
+        its forward ran on (src/chainrules.jl:32-37), whatever tables are set in between."""
+        return (self.table_version, self._table)
+
+    def use_table(self, snap):
+        """Put back the table of table_snapshot() if another one has been set since."""
+        version, table = snap
+        if version != self.table_version:
+            if table[0] == "aniso":
+                self.set_aniso(table[1])
+            else:
+                self.set_vals(table[2], table[1])
         return self
 
     @property

@@ -10,8 +10,8 @@ finishes in seconds:
   dense block against the oracle, and with the configuration's 16384-point dense block through
   invariants (too large for the oracle).
 
-Tolerances: 1e-5 (f32) / 1e-12 (f64) L2-relative, 1e-10 for the f64 d/dvals that include the
-dense matrix adjoint (a different summation order than the oracle's scalar loop).
+Tolerances: 1e-5 (f32) / 1e-12 (f64) L2-relative; the measured error of each comparison is
+printed.
 """
 import sys
 
@@ -86,11 +86,14 @@ def test_k30_f64_matern52_logdet_and_hyperparameters():
     hp = G().to_backend(prob)
     ld, g = G().generate_logdet_and_grad_vals(hp)
     ld_o, g_o = ref.generate_logdet_grad_vals()
+    _say(f"  generate_logdet: relative error {abs(ld - ld_o) / abs(ld_o):.3e} (bar 1e-12)")
     assert abs(ld - ld_o) <= 1e-12 * abs(ld_o)
-    assert relerr(g, g_o) < 1e-10
+    _say(f"  generate_logdet_grad_vals: L2-relative error {relerr(g, g_o):.3e} (bar 1e-12)")
+    assert relerr(g, g_o) < 1e-12
     dh = G().hyperparam_grad(g, table, [1.0, 0.05])
     dh_o = G().hyperparam_grad(g_o, table, [1.0, 0.05])
-    assert relerr(dh, dh_o) < 1e-10
+    _say(f"  hyperparam_grad: L2-relative error {relerr(dh, dh_o):.3e} (bar 1e-12)")
+    assert relerr(dh, dh_o) < 1e-12
     for q, h in ((0, 1e-5), (1, 1e-8)):
         hpp = np.array([1.0, 0.05])
         hpm = hpp.copy()

@@ -2,11 +2,12 @@
 src/chainrules.jl:84-122) through the C ABI, against the oracle and against central differences
 of a continuous-position forward.
 
-Tolerances (L2-relative): 1e-5 in Float32; in Float64 1e-12 for the refinement part and 1e-10
-where the dense layer's K^-1 enters (the library forms it as L^-T L^-1 on the matrix cores, the
-oracle by column solves: a different summation order). The refinement sums each point's terms
-in double in another order than the oracle's pair loop; the oracle runs with its double
-accumulator so that both are compared at the precision of the terms themselves.
+Tolerances (L2-relative): 1e-5 in Float32 and 1e-12 in Float64; the measured error of each
+comparison is printed. Where the dense layer's K^-1 enters, the library forms it as L^-T L^-1 on
+the matrix cores and the oracle by column solves (a different summation order). The refinement
+sums each point's terms in double in another order than the oracle's pair loop; the oracle runs
+with its double accumulator so that both are compared at the precision of the terms
+themselves.
 The reference's own GPU-vs-CPU check of these ops uses rtol 1e-3 (test/runtests.jl:143-157).
 """
 import sys
@@ -59,28 +60,33 @@ def test_point_gradients_vs_oracle(gpu, case, dtype):
     data = rng.standard_normal(N).astype(dtype)
     dord = data[prob.indices]
     f32 = dtype == np.float32
-    t_ref, t_gen = (1e-5, 1e-5) if f32 else (1e-12, 1e-10)
+    t_ref = t_gen = 1e-5 if f32 else 1e-12
+
+    def check(name, a, b, bar):
+        e = relerr(a, b)
+        _say(f"  {name}: L2-relative error {e:.3e} (bar {bar:.0e})")
+        assert e < bar, (name, e)
 
     g = G().refine_logdet_grad_points(hp)
     ld_o, g_o = ref.refine_logdet_grad_points()
     assert g.shape == (N, D)
-    assert relerr(g, g_o) < t_ref, relerr(g, g_o)
+    check("refine_logdet_grad_points", g, g_o, t_ref)
 
     loss, gi = G().refine_inv_loss_grad_points(hp, dord)
     loss_o, gi_o = ref.refine_inv_loss_grad_points(dord)
     assert abs(loss - loss_o) <= t_ref * abs(loss_o)
-    assert relerr(gi, gi_o) < t_ref, relerr(gi, gi_o)
+    check("refine_inv_loss_grad_points", gi, gi_o, t_ref)
 
     ld, gg = G().generate_logdet_and_grad_points(hp)
     ld_o, gg_o = ref.generate_logdet_grad_points()
     assert abs(ld - ld_o) <= t_ref * abs(ld_o)
-    assert relerr(gg, gg_o) < t_gen, relerr(gg, gg_o)
+    check("generate_logdet_grad_points", gg, gg_o, t_gen)
     assert relerr(G().generate_logdet_grad_points(hp), gg) < t_ref  # atomics: order varies
 
     loss, gd = G().generate_inv_loss_grad_points(hp, data)
     loss_o, gd_o = ref.generate_inv_loss_grad_points(data)
     assert abs(loss - loss_o) <= t_ref * abs(loss_o)
-    assert relerr(gd, gd_o) < t_gen, relerr(gd, gd_o)
+    check("generate_inv_loss_grad_points", gd, gd_o, t_gen)
     # the refined rows carry no dense term
     assert relerr(gd[n0:], gi[n0:]) < t_ref
 
