@@ -26,6 +26,9 @@ struct Graph {
     double scale = 0;
     uint32_t* coords = nullptr;    // N*D point-major
     int32_t* nbr = nullptr;        // K*M, nbr[j*M + m]
+    // The stateless entry points' view of a caller's graph: neighbours in the reference's
+    // layout (int64, nbr64[m*K + j]) instead of nbr; only the factor pass reads it.
+    const int64_t* nbr64 = nullptr;
     int32_t* idx = nullptr;        // N, original position of each internal position, or null
     // Internal order = tree order with every refined level sorted along a Morton curve.
     int32_t* i2t = nullptr;        // N, tree position of each internal position, or null

@@ -311,12 +311,25 @@ struct Block {
     T rd[K];            // RN(1 / L[j][j]) for the columns with entries below the diagonal
 
     // _gather_joint! (src/kernels.jl:9-23). nbr is the int32 structure-of-arrays neighbour
-    // table nbr[j*M + m]; coords is point-major.
+    // table nbr[j*M + m]; with nbr64 set, the neighbours come from it instead, in the
+    // reference's layout (int64, the K of a point contiguous: nbr64[m*K + j]). coords is
+    // point-major.
     __device__ inline void gather(const uint32_t* __restrict__ coords,
                                   const int32_t* __restrict__ nbr, int64_t M, int64_t m,
-                                  int64_t n0, int32_t (&nb)[K]) {
+                                  int64_t n0, int32_t (&nb)[K],
+                                  const int64_t* __restrict__ nbr64 = nullptr) {
+        if (nbr64) {
+            // a caller's table is not validated on the host: an index that does not precede
+            // the point is read as the point itself, so no access leaves the arrays
 #pragma unroll
-        for (int j = 0; j < K; ++j) nb[j] = nbr[(int64_t)j * M + m];
+            for (int j = 0; j < K; ++j) {
+                const int64_t q = nbr64[m * K + j];
+                nb[j] = (int32_t)(q >= 0 && q < n0 + m ? q : n0 + m);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < K; ++j) nb[j] = nbr[(int64_t)j * M + m];
+        }
 #pragma unroll
         for (int j = 0; j < K; ++j) {
             const uint32_t* c = coords + (int64_t)nb[j] * D;

@@ -59,13 +59,14 @@ __device__ inline double factor_points(const uint32_t* __restrict__ coords,
                                        const TabParams<T>& P, T* __restrict__ mv,
                                        T* __restrict__ sd, T* __restrict__ terms,
                                        const T* __restrict__ values, T* __restrict__ xi_out,
-                                       const AnisoArgs<T>& an) {
+                                       const AnisoArgs<T>& an,
+                                       const int64_t* __restrict__ nbr64) {
     double lsum = 0.0;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; m < M; m += stride) {
         Block<T, K, D> blk;
         int32_t nb[K];
-        blk.gather(coords, nbr, M, m, n0, nb);
+        blk.gather(coords, nbr, M, m, n0, nb, nbr64);
         if (ANISO) blk.assemble_aniso(scale, an);
         else blk.template assemble<ONE, true>(scale, s_tab, s_acc, P);
         blk.cholesky();
@@ -95,13 +96,15 @@ __device__ inline double factor_points(const uint32_t* __restrict__ coords,
 }
 
 // ANISO: the covariance comes from the anisotropic grid (src/aniso.jl) instead of (bins, vals).
+// nbr64 (optional): the neighbours in the reference's layout (int64, point-major) instead of nbr.
 template <typename T, int K, int D, int MODE, bool ANISO>
 __global__ void __launch_bounds__(kBlock)
 k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, int64_t M,
          int64_t n0, T scale, const TabEnt<T>* __restrict__ g_tab,
          const uint16_t* __restrict__ g_acc, const TabParams<T>* __restrict__ Pp, T* __restrict__ mv,
          T* __restrict__ sd, T* __restrict__ terms, double* __restrict__ partial,
-         const T* __restrict__ values, T* __restrict__ xi_out, AnisoArgs<T> an) {
+         const T* __restrict__ values, T* __restrict__ xi_out, AnisoArgs<T> an,
+         const int64_t* __restrict__ nbr64) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ double s_red[kBlock / 64];
     TabParams<T> P{};
@@ -117,10 +120,12 @@ k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, i
     double lsum = 0.0;
     if (ANISO || P.steps <= 1)
         lsum = factor_points<T, K, D, MODE, ANISO, true>(coords, nbr, M, n0, scale, s_tab, s_acc,
-                                                         P, mv, sd, terms, values, xi_out, an);
+                                                         P, mv, sd, terms, values, xi_out, an,
+                                                         nbr64);
     else
         lsum = factor_points<T, K, D, MODE, ANISO, false>(coords, nbr, M, n0, scale, s_tab, s_acc,
-                                                          P, mv, sd, terms, values, xi_out, an);
+                                                          P, mv, sd, terms, values, xi_out, an,
+                                                          nbr64);
     if (MODE & F_TERMS) {
         const double t = block_sum(lsum, s_red);
         if (threadIdx.x == 0) partial[blockIdx.x] = t;
@@ -530,11 +535,13 @@ void PointK<T, K>::factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T
         if (aniso)                                                                             \
             hipLaunchKernelGGL((k_factor<T, K, DD, MODEV, true>), dim3(nblk), dim3(kBlock), 0,  \
                                st, g.coords, g.nbr, g.M, g.n0, scale, tb.tab, tb.acc,           \
-                               tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso);    \
+                               tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso,     \
+                               g.nbr64);                                                        \
         else                                                                                   \
             hipLaunchKernelGGL((k_factor<T, K, DD, MODEV, false>), dim3(nblk), dim3(kBlock),    \
                                lds, st, g.coords, g.nbr, g.M, g.n0, scale, tb.tab, tb.acc,      \
-                               tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso);    \
+                               tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso,     \
+                               g.nbr64);                                                        \
     } while (0)
 #define GGP_FACTOR_D(DD)                                                                       \
     switch (mode) {                                                                            \

@@ -44,14 +44,21 @@ __device__ inline double wave_sum(double v) {
 
 // Joint coordinates of row `lane`: neighbour `lane` for lane < k, the point itself otherwise
 // (_gather_joint!, src/kernels.jl:9-23). Returns the neighbour index (-1 for the point row).
+// nbr64 (optional): the neighbours in the reference's layout, int64 nbr64[m*K + j].
 template <int D>
 __device__ inline int32_t wide_gather(uint32_t (&x)[D], const uint32_t* __restrict__ coords,
                                       const int32_t* __restrict__ nbr, int64_t M, int64_t m,
-                                      int64_t n0, int K, int lane) {
+                                      int64_t n0, int K, int lane,
+                                      const int64_t* __restrict__ nbr64 = nullptr) {
     int32_t nb = -1;
     int64_t row = n0 + m;
     if (lane < K) {
-        nb = nbr[(int64_t)lane * M + m];
+        if (nbr64) {  // not validated on the host: an index that does not precede the point
+            const int64_t q = nbr64[m * K + lane];  // is read as the point itself
+            nb = (int32_t)(q >= 0 && q < n0 + m ? q : n0 + m);
+        } else {
+            nb = nbr[(int64_t)lane * M + m];
+        }
         row = nb;
     }
     const uint32_t* c = coords + row * D;
@@ -143,7 +150,7 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
            const uint16_t* __restrict__ g_acc, const TabParams<T>* __restrict__ Pp,
            T* __restrict__ mv, T* __restrict__ sd, T* __restrict__ terms,
            double* __restrict__ partial, const T* __restrict__ values, T* __restrict__ xi_out,
-           AnisoArgs<T> an) {
+           AnisoArgs<T> an, const int64_t* __restrict__ nbr64) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ double s_red[kWideWaves];
     TabParams<T> P{};
@@ -161,7 +168,7 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
     const int64_t wstride = (int64_t)gridDim.x * kWideWaves;
     for (int64_t m = (int64_t)blockIdx.x * kWideWaves + (threadIdx.x >> 6); m < M; m += wstride) {
         uint32_t x[D];
-        const int32_t nb = wide_gather<D>(x, coords, nbr, M, m, n0, K, lane);
+        const int32_t nb = wide_gather<D>(x, coords, nbr, M, m, n0, K, lane, nbr64);
         T a[kWideN], unused[kWideN];
         wide_assemble<T, D, ANISO>(a, x, n, lane, scale, s_tab, s_acc, P, an);
         const T s = wide_cholesky<T, false>(a, unused, n, K, lane);

@@ -29,11 +29,13 @@ void WideD<T, D>::factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T*
         if (aniso)                                                                             \
             hipLaunchKernelGGL((k_factor_w<T, DD, MODEV, true>), dim3(grid), dim3(kWideBlock),  \
                                0, st, g.coords, g.nbr, g.M, g.n0, K, scale, tb.tab, tb.acc,     \
-                               tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso);    \
+                               tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso,     \
+                               g.nbr64);                                                        \
         else                                                                                   \
             hipLaunchKernelGGL((k_factor_w<T, DD, MODEV, false>), dim3(grid), dim3(kWideBlock), \
                                lds, st, g.coords, g.nbr, g.M, g.n0, K, scale, tb.tab, tb.acc,   \
-                               tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso);    \
+                               tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso,     \
+                               g.nbr64);                                                        \
     } while (0)
 #define GGP_FACTOR_W_D(DD)                                                                     \
     switch (mode) {                                                                            \

@@ -73,6 +73,15 @@ _HIP_SIGS = {
     "ggp_generate_inv_loss_grad_points": (C.c_int, [_P, _P, _P, _DP, _P]),
     "ggp_build_graph_device": (C.c_int, [_P, _I64, _I32, _I64, _I64, _I32, _P, _P, _P, _P, _I64,
                                          C.POINTER(_I64), _DP, _P]),
+    # stateless entry points with the reference's accelerator signatures
+    "gphip_refine_logdet_f32": (C.c_int, [_P, C.c_float, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                          _I64, _P]),
+    "gphip_refine_inv_f32": (C.c_int, [_P, C.c_float, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                       _I64, _P]),
+    "gphip_refine_logdet_f64": (C.c_int, [_P, C.c_double, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                          _I64, _P]),
+    "gphip_refine_inv_f64": (C.c_int, [_P, C.c_double, _P, _P, _P, _P, _P, _I64, _I64, _I64,
+                                       _I64, _I64, _P]),
 }
 
 _GRAPH_SIGS = {

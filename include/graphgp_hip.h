@@ -165,6 +165,44 @@ int ggp_refine_inv_loss_grad_points(ggp_graph* h, const void* values_tree, void*
 int ggp_generate_inv_loss_grad_points(ggp_graph* h, const void* data, void* d_points,
                                       double* loss_host, void* stream);
 
+/* ---- stateless entry points with the reference's accelerator signatures --------------------
+ * gpcuda_refine_logdet_f32 / gpcuda_refine_inv_f32 (csrc/graphgp_capi.cu:70-94, bound by
+ * refine_logdet_custom / refine_inv_custom, ext/GraphGPCUDAExt.jl:38-63): the order-independent
+ * per-point ops over all M = n_points - n0 refined points in one launch, on the caller's device
+ * arrays, with no problem handle. The one change of signature: the reference passes float
+ * positions (scale * coords, csrc/graphgp_capi.cu:10-13), which do not reproduce the lattice
+ * lookup (src/linalg.jl:19-24); these take the integer lattice `coords` and `scale` instead.
+ *   coords     device, n_points * ndim uint32, point-major, tree order (the reference's (D, N)
+ *              column-major prob.coords)
+ *   neighbors  device, (n_points - n0) * k int64, point-major, 0-based (prob.neighbors .- 1);
+ *              each index must precede its point (an index that does not is read as the point
+ *              itself, so no access leaves the arrays, and that point's result is meaningless)
+ *   cov_bins / cov_vals  device, n_cov entries (prob.bins / prob.vals), bins strictly
+ *              increasing with bins[0] = 0; not validated on the host
+ *   out        device, 1 entry: sum over the refined points of log std (refine_logdet)
+ *   values / xi  device, n_points / (n_points - n0) entries: refine_inv, tree order
+ * Asynchronous on `stream` (a hipStream_t; NULL = default stream), as the reference's; the
+ * scratch they need (the prepared table and partial sums, a few tens of KiB) is allocated and
+ * released stream-ordered on that stream. Returns 0, 2 (k outside 1..31), 3 (ndim not 2, 3 or
+ * 4), 7 (other argument) or 5 (HIP error). */
+int gphip_refine_logdet_f32(const uint32_t* coords, float scale, const int64_t* neighbors,
+                            const float* cov_bins, const float* cov_vals, float* out, int64_t n0,
+                            int64_t k, int64_t n_points, int64_t n_cov, int64_t ndim,
+                            void* stream);
+int gphip_refine_inv_f32(const uint32_t* coords, float scale, const int64_t* neighbors,
+                         const float* cov_bins, const float* cov_vals, const float* values,
+                         float* xi, int64_t n0, int64_t k, int64_t n_points, int64_t n_cov,
+                         int64_t ndim, void* stream);
+/* The same in Float64 (no counterpart in the reference's ABI, which is Float32 only). */
+int gphip_refine_logdet_f64(const uint32_t* coords, double scale, const int64_t* neighbors,
+                            const double* cov_bins, const double* cov_vals, double* out,
+                            int64_t n0, int64_t k, int64_t n_points, int64_t n_cov,
+                            int64_t ndim, void* stream);
+int gphip_refine_inv_f64(const uint32_t* coords, double scale, const int64_t* neighbors,
+                         const double* cov_bins, const double* cov_vals, const double* values,
+                         double* xi, int64_t n0, int64_t k, int64_t n_points, int64_t n_cov,
+                         int64_t ndim, void* stream);
+
 /* ---- graph build on the device ----------------------------------------------------------
  * build_graph (src/graph_build.jl:254-288) on the GPU; replaces gpcuda_build_graph_f32
  * (csrc/graphgp_capi.cu:100-117, driven by build_graph_cuda, ext/GraphGPCUDAExt.jl:66-105).

@@ -18,7 +18,7 @@ HEADERS = [os.path.join(ROOT, "include", h) for h in ("graphgp_hip.h", "graphgp_
 def declared(path):
     text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return re.findall(r"\b(ggp_[a-z_0-9]+)\s*\(", text)
+    return re.findall(r"\b((?:ggp|gphip)_[a-z_0-9]+)\s*\(", text)
 
 
 @pytest.mark.parametrize("header", HEADERS, ids=os.path.basename)
@@ -74,3 +74,24 @@ def test_ops_require_a_device_problem():
                             float(z["scale"]), z["cov_bins32"], z["cov_vals32"])
     with pytest.raises(TypeError):
         G.generate(prob, np.zeros(prob.N, np.float32))
+
+
+def test_stateless_entry_points_reject_bad_arguments_before_any_device_call():
+    """gphip_refine_logdet_f32 / gphip_refine_inv_f32 return the reference's codes for an
+    unsupported k (2) or ndim (3) (csrc/graphgp_capi.cu:53-68) and 7 for a null array, before
+    any HIP call."""
+    lib = nat.hip()
+    f32 = C.c_float(1e-6)
+    dummy = C.c_void_p(16)  # never dereferenced: every case below is rejected first
+    for fn in (lib.gphip_refine_logdet_f32, lib.gphip_refine_logdet_f64):
+        sc = f32 if fn is lib.gphip_refine_logdet_f32 else C.c_double(1e-6)
+        assert fn(dummy, sc, dummy, dummy, dummy, dummy, 10, 32, 100, 50, 3, None) == 2
+        assert fn(dummy, sc, dummy, dummy, dummy, dummy, 10, 0, 100, 50, 3, None) == 2
+        assert fn(dummy, sc, dummy, dummy, dummy, dummy, 10, 8, 100, 50, 5, None) == 3
+        assert fn(None, sc, dummy, dummy, dummy, dummy, 10, 8, 100, 50, 3, None) == 7
+        assert fn(dummy, sc, dummy, dummy, dummy, dummy, 10, 8, 100, 1, 3, None) == 7
+    assert lib.gphip_refine_inv_f32(dummy, f32, dummy, dummy, dummy, None, dummy, 10, 8, 100, 50,
+                                    3, None) == 7
+    assert lib.gphip_refine_inv_f32(dummy, f32, dummy, dummy, dummy, dummy, dummy, 10, 8, 100,
+                                    50, 1, None) == 3
+    assert b"ndim" in lib.ggp_last_error()
