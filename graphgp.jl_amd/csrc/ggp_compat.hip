@@ -13,10 +13,14 @@
 // Scratch (bytes from offset 0): [TabParams | TabEnt x (nb-1) | uint16 cell index x (U+1) |
 // double partial sums x nblk], each part 256-byte aligned. The entry points allocate it
 // stream-ordered (hipMallocAsync / hipFreeAsync) on the caller's stream; nothing else is
-// allocated and nothing is synchronized.
+// allocated and nothing is synchronized. gphip_refine_logdet_f32_noalloc instead uses a fixed
+// 64 KiB device array of this file (tables of at most 2048 bins): every byte a call reads is
+// written earlier in the same call, so nothing needs clearing, and calls that overlap on one
+// device race on it.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "../../include/graphgp_hip.h"
@@ -254,6 +258,55 @@ int enqueue(const CompatArgs& a, int op, unsigned char* scratch, int cells, unsi
     return 0;
 }
 
+// ---- the allocation-free variant --------------------------------------------------------------
+// One file-scope device array serves every call on a device (each device holds its own copy
+// until the process ends). Host code never passes the array's name: its device address is taken
+// once per device with hipGetSymbolAddress and kept here.
+constexpr size_t kNoAllocBytes = 64 * 1024;
+constexpr int64_t kNoAllocMaxBins = 2048;  // f32 table that, with the index and partial sums, fits
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_device(unsigned char** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(GGP_ERR_HIP, "hipGetDevice failed");
+    if (dev < 0 || dev >= kMaxDevices) return set_error(GGP_ERR_HIP, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(GGP_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") +
+                                              hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = static_cast<unsigned char*>(g_scratch_ptr[dev]);
+    return 0;
+}
+
+template <typename T>
+int run_noalloc(const CompatArgs& a, int op, hipStream_t st) {
+    if (int rc = check(a, op)) return rc;
+    if (a.nb > kNoAllocMaxBins)
+        return set_error(GGP_ERR_ARG, "n_cov above 2048: the allocation-free entry point's fixed "
+                                      "scratch holds tables of at most 2048 bins");
+    DevInfo d;
+    if (int rc = dev_info(d)) return rc;
+    int cells = 0;
+    unsigned nblk = 0;
+    const size_t bytes = scratch_bytes<T>(a, d, &cells, &nblk);
+    if (!bytes) return GGP_ERR_ARG;
+    if (bytes > kNoAllocBytes)
+        return set_error(GGP_ERR_ARG, "problem needs more scratch than the allocation-free entry "
+                                      "point's fixed 64 KiB");
+    unsigned char* p = nullptr;
+    if (int rc = scratch_of_device(&p)) return rc;
+    return enqueue<T>(a, op, p, cells, nblk, st);
+}
+
 template <typename T>
 int run_alloc(const CompatArgs& a, int op, hipStream_t st) {
     if (int rc = check(a, op)) return rc;
@@ -287,6 +340,15 @@ int gphip_refine_logdet_f32(const uint32_t* coords, float scale, const int64_t* 
     const CompatArgs a{coords, (double)scale, neighbors, cov_bins, cov_vals, nullptr, out,
                        n0, k, n_points, n_cov, ndim};
     return ggp::run_alloc<float>(a, ggp::C_LOGDET, (hipStream_t)stream);
+}
+
+int gphip_refine_logdet_f32_noalloc(const uint32_t* coords, float scale,
+                                    const int64_t* neighbors, const float* cov_bins,
+                                    const float* cov_vals, float* out, int64_t n0, int64_t k,
+                                    int64_t n_points, int64_t n_cov, int64_t ndim, void* stream) {
+    const CompatArgs a{coords, (double)scale, neighbors, cov_bins, cov_vals, nullptr, out,
+                       n0, k, n_points, n_cov, ndim};
+    return ggp::run_noalloc<float>(a, ggp::C_LOGDET, (hipStream_t)stream);
 }
 
 int gphip_refine_inv_f32(const uint32_t* coords, float scale, const int64_t* neighbors,

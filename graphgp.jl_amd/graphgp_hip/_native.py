@@ -78,6 +78,8 @@ _HIP_SIGS = {
                                           _I64, _P]),
     "gphip_refine_inv_f32": (C.c_int, [_P, C.c_float, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                        _I64, _P]),
+    "gphip_refine_logdet_f32_noalloc": (C.c_int, [_P, C.c_float, _P, _P, _P, _P, _I64, _I64, _I64,
+                                                  _I64, _I64, _P]),
     "gphip_refine_logdet_f64": (C.c_int, [_P, C.c_double, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                           _I64, _P]),
     "gphip_refine_inv_f64": (C.c_int, [_P, C.c_double, _P, _P, _P, _P, _P, _I64, _I64, _I64,

@@ -193,6 +193,17 @@ int gphip_refine_inv_f32(const uint32_t* coords, float scale, const int64_t* nei
                          const float* cov_bins, const float* cov_vals, const float* values,
                          float* xi, int64_t n0, int64_t k, int64_t n_points, int64_t n_cov,
                          int64_t ndim, void* stream);
+/* No counterpart in the reference: gphip_refine_logdet_f32 for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments and result; the scratch is a fixed 64 KiB device array of the
+ * library (one per device, held until the process ends) instead of a stream-ordered allocation,
+ * and no allocating routine is called. Limit: n_cov <= 2048 (status 7 beyond). Every call on a
+ * device shares that array, so calls that overlap on one device (different streams or host
+ * threads) race and must be serialized by the caller. */
+int gphip_refine_logdet_f32_noalloc(const uint32_t* coords, float scale,
+                                    const int64_t* neighbors, const float* cov_bins,
+                                    const float* cov_vals, float* out, int64_t n0, int64_t k,
+                                    int64_t n_points, int64_t n_cov, int64_t ndim, void* stream);
 /* The same in Float64 (no counterpart in the reference's ABI, which is Float32 only). */
 int gphip_refine_logdet_f64(const uint32_t* coords, double scale, const int64_t* neighbors,
                             const double* cov_bins, const double* cov_vals, double* out,
