@@ -16,6 +16,7 @@
 
 #include "../../include/graphgp_hip.h"
 #include "ggp_internal.h"
+#include "ggp_pack.h"
 
 using namespace ggp;
 
@@ -71,8 +72,9 @@ struct ggp_graph {
     int* hinfo = nullptr;            // host mirror of info
     int* herr = nullptr;             // host mirror of the sweep error flags (dstat + 80)
     int* dsync = nullptr;            // dense Cholesky task counter and tile flags
-    double* hist = nullptr;          // (nblk_pull + nw_dense) x nb
+    double* hist = nullptr;          // (pull_blocks + nw_dense) x nb
     int hist_nb = 0;
+    unsigned hist_rows = 0;
     double *W = nullptr, *C = nullptr, *Q = nullptr, *u = nullptr;  // dense f64 scratch (lazy)
     double *dp = nullptr, *dpd = nullptr;  // d/dpoints accumulators, N x D and n0 x D (lazy)
     std::vector<void*> owned;
@@ -86,9 +88,21 @@ struct ggp_graph {
 
 namespace {
 
+constexpr int64_t kMinLdsCells = 512;     // fewer cells of LDS index than this: table in global
+constexpr unsigned kGlobalPullBlocks = 256;
+
 template <typename T> Table<T>& table(ggp_graph* h);
 template <> Table<float>& table<float>(ggp_graph* h) { return h->tf; }
 template <> Table<double>& table<double>(ggp_graph* h) { return h->td; }
+
+bool table_global(const ggp_graph* h) { return h->dtype == GGP_F32 ? h->tf.global : h->td.global; }
+
+// Workgroups (and histogram rows) of the adjoint pass. With the table in global memory each row
+// is zeroed and accumulated by atomics and every row is reduced, so fewer rows are used.
+unsigned pull_blocks(const ggp_graph* h, bool global) {
+    return global ? std::min<unsigned>(h->nblk_pull, kGlobalPullBlocks) : h->nblk_pull;
+}
+unsigned pull_blocks(const ggp_graph* h) { return pull_blocks(h, table_global(h)); }
 
 constexpr size_t kStatBytes = 96;
 
@@ -101,6 +115,17 @@ int dmalloc(ggp_graph* h, void** p, size_t bytes) {
     }
     h->owned.push_back(*p);
     return 0;
+}
+
+// Release a buffer of the handle (set_cov replacing a table; every op has finished by then:
+// ops return after their work is done).
+void dfree(ggp_graph* h, void* p) {
+    if (!p) return;
+    auto it = std::find(h->owned.begin(), h->owned.end(), p);
+    if (it != h->owned.end()) {
+        h->owned.erase(it);
+        (void)hipFree(p);
+    }
 }
 
 void free_all(ggp_graph* h) {
@@ -163,7 +188,12 @@ int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
     const size_t slack = 512 + (size_t)kWideBlock / 64 * 2 * 64 * sizeof(T);
     size_t budget = h->lds_max > entb + (size_t)nb * 8 + slack ? h->lds_max - entb - (size_t)nb * 8 - slack : 0;
     int64_t umax = std::min<int64_t>(4096, (int64_t)(budget / 2) - 1);
-    if (umax < 1) return fail(GGP_ERR_ARG, "covariance table too large for LDS");
+    // Too little LDS left for a useful cell index: the table stays in global memory (the
+    // reference's lookups read it there for any nbins, src/interp.jl:10-34; its gradients fall
+    // back to global atomics beyond its shared-memory histogram, src/grad.jl:107-116), with a
+    // finer index there.
+    const bool global = umax < kMinLdsCells;
+    if (global) umax = std::min<int64_t>(65536, std::max<int64_t>(4096, 4 * nb));
     int shift = 0;
     while ((int64_t)(range >> shift) + 1 > umax) ++shift;
     const int ucells = (int)((range >> shift) + 1);
@@ -199,7 +229,11 @@ int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
     P.ucells = ucells;
     P.nb = (int)nb;
     const bool realloc_tab = !tb.tab || tb.P.nb != (int)nb || tb.P.ucells != ucells;
-    if (realloc_tab) {
+    if (realloc_tab) {  // the previous table's buffers are released (ops have finished)
+        dfree(h, tb.tab);
+        dfree(h, tb.acc);
+        tb.tab = nullptr;
+        tb.acc = nullptr;
         if (dmalloc(h, (void**)&tb.tab, entb)) return GGP_ERR_HIP;
         if (dmalloc(h, (void**)&tb.acc, acc.size() * sizeof(uint16_t))) return GGP_ERR_HIP;
         if (!tb.params && dmalloc(h, (void**)&tb.params, sizeof(TabParams<T>))) return GGP_ERR_HIP;
@@ -208,15 +242,20 @@ int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
     HC(hipMemcpy(tb.acc, acc.data(), acc.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
     HC(hipMemcpy(tb.params, &P, sizeof(P), hipMemcpyHostToDevice));
     tb.P = P;
+    tb.global = global;
     tb.bins.assign(bins, bins + nb);
     tb.vals.assign(vals, vals + nb);
+    dfree(h, const_cast<T*>(tb.aniso.sb));  // an anisotropic table set before
     tb.aniso = AnisoArgs<T>{};
     tb.aniso_host.clear();
-    if (h->hist_nb != (int)nb) {
-        if (dmalloc(h, (void**)&h->hist,
-                    (size_t)(h->nblk_pull + h->nw_dense) * (size_t)nb * sizeof(double)))
+    const unsigned rows = pull_blocks(h, global) + (unsigned)h->nw_dense;
+    if (h->hist_nb != (int)nb || h->hist_rows != rows) {
+        dfree(h, h->hist);
+        h->hist = nullptr;
+        if (dmalloc(h, (void**)&h->hist, (size_t)rows * (size_t)nb * sizeof(double)))
             return GGP_ERR_HIP;
         h->hist_nb = (int)nb;
+        h->hist_rows = rows;
     }
     h->has_cov = true;
     return 0;
@@ -224,9 +263,9 @@ int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
 
 // ---- kernel timers ---------------------------------------------------------------------------
 enum Timer { TM_FACTOR = 0, TM_PULLBACK = 1, TM_SWEEP_FWD = 2, TM_SWEEP_REV = 3, TM_DENSE = 4,
-             TM_OP = 5, TM_COUNT = 6 };
+             TM_OP = 5, TM_POTRF = 6, TM_COUNT = 7 };
 const char* const kTimerNames[TM_COUNT] = {"factor", "pullback", "sweep_fwd", "sweep_rev",
-                                           "dense", "op"};
+                                           "dense", "op", "potrf"};
 
 inline void tstart(ggp_graph* h, int t, hipStream_t st) {
     if (h->timing >> t & 1) (void)hipEventRecord(h->tev[2 * t], st);
@@ -271,6 +310,8 @@ int set_cov_aniso(ggp_graph* h, const T* sb, int64_t ns, const T* zb, int64_t nz
     for (const T& x : host)
         if (!std::isfinite(x)) return fail(GGP_ERR_ARG, "aniso table must be finite");
     T* dev = nullptr;
+    dfree(h, const_cast<T*>(tb.aniso.sb));  // the previous anisotropic table
+    tb.aniso = AnisoArgs<T>{};
     if (dmalloc(h, (void**)&dev, host.size() * sizeof(T))) return GGP_ERR_HIP;
     HC(hipMemcpy(dev, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice));
     tb.aniso.sb = dev;
@@ -280,6 +321,7 @@ int set_cov_aniso(ggp_graph* h, const T* sb, int64_t ns, const T* zb, int64_t nz
     tb.aniso.nz = (int)nz;
     tb.aniso.alpha = (T)alpha;
     tb.aniso_host = host;
+    tb.global = false;
     // the isotropic table is not used by an anisotropic problem
     tb.vals.assign(1, grid[0]);
     h->has_cov = true;
@@ -384,7 +426,9 @@ template <typename T>
 void dense_factor_async(ggp_graph* h, hipStream_t st) {
     tstart(h, TM_DENSE, st);
     dense_assemble<T>(h->g, table<T>(h), tp<T>(h->A), T(0), st, h->info, h->dsync);
+    tstart(h, TM_POTRF, st);
     dense_potrf<T>(tp<T>(h->A), (int)h->g.n0, h->info, h->dsync, dense_wgs(h), st, true);
+    tstop(h, TM_POTRF, st);
     tstop(h, TM_DENSE, st);
 }
 
@@ -400,7 +444,7 @@ void factor_t(ggp_graph* h, int mode, T* mv, T* sd, T* terms, double* partial, c
 template <typename T>
 void pullback_t(ggp_graph* h, int mode, const T* v, const T* xi, const T* vb) {
     tstart(h, TM_PULLBACK, h->s_main);
-    launch_pullback<T>(h->g, table<T>(h), mode, v, xi, vb, h->hist, h->scal_partial, h->nblk_pull,
+    launch_pullback<T>(h->g, table<T>(h), mode, v, xi, vb, h->hist, h->scal_partial, pull_blocks(h),
                        h->s_main);
     tstop(h, TM_PULLBACK, h->s_main);
 }
@@ -634,7 +678,7 @@ template <typename T>
 void dense_grad(ggp_graph* h, int kind, hipStream_t st, bool inverse_ready = false) {
     const Graph& g = h->g;
     const Table<T>& tb = table<T>(h);
-    double* rows = h->hist + (size_t)h->nblk_pull * h->hist_nb;
+    double* rows = h->hist + (size_t)pull_blocks(h) * h->hist_nb;
     const int n = (int)g.n0;
     if (kind == DG_LOGDET) {
         dense_logdiag<T>(tp<T>(h->A), n, h->dscal + 1, st);
@@ -716,12 +760,12 @@ int op_grad_vals(ggp_graph* h, int mode, int dkind, const T* in1, const T* in2, 
     if (g.M > 0)
         pullback_t<T>(h, mode, pull_v, xt, vb);
     else
-        launch_fill<double>(h->hist, 0.0, (int64_t)h->nblk_pull * nb, h->s_main);
+        launch_fill<double>(h->hist, 0.0, (int64_t)pull_blocks(h) * nb, h->s_main);
     if (mode != P_GENVALS && g.M > 0)
-        launch_reduce_scalar(h->dscal, h->scal_partial, (int)h->nblk_pull, nullptr, h->s_main);
+        launch_reduce_scalar(h->dscal, h->scal_partial, (int)pull_blocks(h), nullptr, h->s_main);
     if (dkind != DG_NONE)
         if (int rc = join(h)) return rc;
-    const int rows = (int)h->nblk_pull + (dkind != DG_NONE ? h->nw_dense : 0);
+    const int rows = (int)pull_blocks(h) + (dkind != DG_NONE ? h->nw_dense : 0);
     launch_reduce_hist<T>(d_vals, h->hist, rows, nb, nullptr, h->s_main);
     if (int rc = finish(h, user)) return rc;
     if (dkind != DG_NONE && *h->hinfo != 0) {
@@ -801,9 +845,9 @@ int op_grad_points(ggp_graph* h, int mode, bool dense, const T* in, T* d_points,
     if (g.M > 0) {
         tstart(h, TM_PULLBACK, h->s_main);
         launch_pullback<T>(g, tb, mode | P_PTS, pull_v, nullptr, nullptr, h->dp, h->scal_partial,
-                           h->nblk_pull, h->s_main);
+                           pull_blocks(h), h->s_main);
         tstop(h, TM_PULLBACK, h->s_main);
-        launch_reduce_scalar(h->dscal, h->scal_partial, (int)h->nblk_pull, nullptr, h->s_main);
+        launch_reduce_scalar(h->dscal, h->scal_partial, (int)pull_blocks(h), nullptr, h->s_main);
     }
     if (dense)
         if (int rc = join(h)) return rc;
@@ -832,43 +876,10 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     if (!supported_d(D)) return fail(GGP_ERR_D, "unsupported D (supported: 2, 3, 4)");
     if (dtype != GGP_F32 && dtype != GGP_F64) return fail(GGP_ERR_ARG, "dtype must be GGP_F32 or GGP_F64");
     if (!(std::isfinite(scale) && scale > 0)) return fail(GGP_ERR_ARG, "scale must be finite and > 0");
-    if (N < 1 || n0 < 1 || n0 > N) return fail(GGP_ERR_GRAPH, "need 1 <= n0 <= N");
-    if (N > INT32_MAX) return fail(GGP_ERR_ARG, "N must fit in int32");
-    if (n0 > 16384) return fail(GGP_ERR_ARG, "n0 above 16384 is not supported");
+    std::string err;
+    if (int rc = check_graph_host(coords, nbrs, offs, n_off, indices, n0, k, N, D, &err))
+        return fail(rc, err);
     const int64_t M = N - n0;
-    if ((uint64_t)M * (uint64_t)k >= (1ull << 32)) return fail(GGP_ERR_ARG, "M*k must be < 2^32");
-    if (!coords || (M > 0 && !nbrs) || !offs) return fail(GGP_ERR_ARG, "null input array");
-    // check_graph (src/graph_build.jl:20-57)
-    if (n_off < 1) return fail(GGP_ERR_GRAPH, "offsets is empty");
-    if (offs[0] != n0) return fail(GGP_ERR_GRAPH, "offsets[0] must equal n0");
-    for (int64_t b = 1; b < n_off; ++b)
-        if (offs[b] < offs[b - 1]) return fail(GGP_ERR_GRAPH, "offsets must be non-decreasing");
-    if (offs[n_off - 1] > N) return fail(GGP_ERR_GRAPH, "offsets[end] must be <= N");
-    {
-        int64_t b = 1;
-        for (int64_t m = 0; m < M; ++m) {
-            const int64_t p = n0 + m;
-            while (b < n_off && offs[b] <= p) ++b;
-            const int64_t prev_end = b < n_off ? offs[b - 1] : offs[n_off - 1];
-            for (int64_t j = 0; j < k; ++j) {
-                const int64_t q = nbrs[m * k + j];
-                if (q < 0 || q >= N) return fail(GGP_ERR_GRAPH, "neighbour index out of range");
-                if (q >= p) return fail(GGP_ERR_GRAPH, "neighbour does not precede its point (not topological)");
-                if (b < n_off && q >= prev_end)
-                    return fail(GGP_ERR_GRAPH, "neighbour in its own depth level; neighbours must be in earlier levels");
-            }
-        }
-    }
-    if (indices) {
-        std::vector<char> seen((size_t)N, 0);
-        for (int64_t i = 0; i < N; ++i) {
-            if (indices[i] < 0 || indices[i] >= N || seen[(size_t)indices[i]])
-                return fail(GGP_ERR_GRAPH, "indices must be a permutation of 0..N-1");
-            seen[(size_t)indices[i]] = 1;
-        }
-    }
-    for (int64_t i = 0; i < N * D; ++i)
-        if (coords[i] >= (1u << 25)) return fail(GGP_ERR_ARG, "lattice coordinates must be < 2^25");
 
     ggp_graph* h = new ggp_graph();
     auto bail = [&](int rc) { free_all(h); delete h; return rc; };
@@ -896,126 +907,23 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     g.N = N; g.n0 = n0; g.M = M; g.K = k; g.D = D; g.scale = scale;
     g.offsets.assign(offs, offs + n_off);
     const size_t es = dtype == GGP_F32 ? 4 : 8;
-    // Internal order: inside every refined depth level the points are ordered along a Morton
-    // curve of their lattice coordinates, so that the points a chunk of lanes handles are
-    // neighbours in space and their gathers (neighbour coordinates and values, consumers) share
-    // cache lines. The dense block and any points past the last level keep their positions. No
-    // result depends on this order: per-point arithmetic is unchanged and every list keeps the
-    // reference's order; ops translate at their boundary (i2t: internal -> tree position).
-    std::vector<int32_t> i2t((size_t)N), t2i((size_t)N);
-    for (int64_t i = 0; i < N; ++i) i2t[(size_t)i] = (int32_t)i;
-    const bool relabel = M > 0 && !std::getenv("GGP_TREE_ORDER");
-    if (relabel) {
-        uint32_t cmax = 0;
-        for (int64_t i = 0; i < N * D; ++i) cmax = std::max(cmax, coords[i]);
-        int cbits = 0;
-        while (cbits < 32 && (cmax >> cbits) != 0) ++cbits;
-        const int per = 63 / D;
-        const int drop = std::max(0, cbits - per);
-        std::vector<uint64_t> key((size_t)N, 0);
-        for (int64_t i = n0; i < N; ++i) {
-            uint64_t kk = 0;
-            for (int b = per - 1; b >= 0; --b)
-                for (int d = 0; d < D; ++d)
-                    kk = (kk << 1) | ((coords[i * D + d] >> (b + drop)) & 1u);
-            key[(size_t)i] = kk;
-        }
-        for (int64_t b = 1; b < n_off; ++b) {
-            const int64_t lo = offs[b - 1], hi = offs[b];
-            std::stable_sort(i2t.begin() + lo, i2t.begin() + hi,
-                             [&](int32_t a, int32_t c) { return key[(size_t)a] < key[(size_t)c]; });
-        }
-    }
-    for (int64_t i = 0; i < N; ++i) t2i[(size_t)i2t[(size_t)i]] = (int32_t)i;
-    // neighbours: int32 structure of arrays, internal indices
-    std::vector<int32_t> nsoa((size_t)(M * k));
-    for (int64_t m = 0; m < M; ++m) {
-        const int64_t mt = i2t[(size_t)(n0 + m)] - n0;  // tree index of internal m
-        for (int64_t j = 0; j < k; ++j)
-            nsoa[(size_t)(j * M + m)] = t2i[(size_t)nbrs[mt * k + j]];
-    }
-    // reverse neighbour list over the points that lie in a level, consumers by decreasing tree
-    // position (entries m*k + j with internal m), indexed by internal q
-    const int64_t mlev = std::max<int64_t>(0, offs[n_off - 1] - n0);
-    std::vector<int64_t> rptr((size_t)N + 1, 0);
-    for (int64_t m = 0; m < mlev; ++m)
-        for (int64_t j = 0; j < k; ++j) rptr[(size_t)t2i[(size_t)nbrs[m * k + j]] + 1]++;
-    for (int64_t q = 0; q < N; ++q) rptr[(size_t)q + 1] += rptr[(size_t)q];
-    std::vector<uint32_t> revl((size_t)std::max<int64_t>(rptr[(size_t)N], 1));
-    {
-        std::vector<int64_t> pos(rptr.begin(), rptr.end() - 1);
-        for (int64_t m = mlev - 1; m >= 0; --m) {
-            const int64_t mi = t2i[(size_t)(n0 + m)] - n0;
-            for (int64_t j = 0; j < k; ++j) {
-                const int64_t q = t2i[(size_t)nbrs[m * k + j]];
-                revl[(size_t)pos[(size_t)q]++] = (uint32_t)(mi * k + j);
-            }
-        }
-    }
-    std::vector<uint32_t> rcnt((size_t)N);
-    for (int64_t q = 0; q < N; ++q) rcnt[(size_t)q] = (uint32_t)(rptr[(size_t)q + 1] - rptr[(size_t)q]);
-    // Chunk lists of the one-launch sweeps (within one level each, topological order).
-    std::vector<int4> fch, rch;
-    for (int64_t b = 1; b < n_off; ++b)
-        for (int64_t s0 = offs[b - 1]; s0 < offs[b]; s0 += kBlock)
-            fch.push_back(make_int4((int)(s0 - n0), (int)std::min<int64_t>(kBlock, offs[b] - s0), 0, 0));
-    // Reverse chunks: the fewest lanes per point (2^lg) that keep every lane at kRevSlots list
-    // entries or fewer (at most 64 lanes; longer lists take several rounds).
-    std::vector<uint32_t> rev;
-    for (int64_t b = n_off - 1; b >= 0; --b) {
-        const int64_t lo = b == 0 ? 0 : offs[b - 1], hi = b == 0 ? n0 : offs[b];
-        for (int64_t s0 = lo; s0 < hi;) {
-            int lg = 0;
-            int64_t np = 0, maxc = 0;
-            for (;; ++lg) {
-                np = std::min<int64_t>(kBlock >> lg, hi - s0);
-                maxc = 0;
-                for (int64_t q = s0; q < s0 + np; ++q) maxc = std::max<int64_t>(maxc, rcnt[(size_t)q]);
-                if (((maxc + (1 << lg) - 1) >> lg) <= kRevSlots || lg == 6) break;
-            }
-            const int64_t nslots = (maxc + (1 << lg) - 1) >> lg;
-            const int64_t base = (int64_t)rev.size();
-            if (base + nslots * kBlock >= ((int64_t)1 << 31))
-                return bail(fail(GGP_ERR_ARG, "reverse neighbour lists too large"));
-            rev.resize((size_t)(base + nslots * kBlock), kRevNone);
-            for (int64_t i = 0; i < np; ++i) {
-                const int64_t q = s0 + i;
-                for (int64_t u = 0; u < (int64_t)rcnt[(size_t)q]; ++u) {
-                    const int64_t lane = (i << lg) + (u & ((1 << lg) - 1));
-                    rev[(size_t)(base + (u >> lg) * kBlock + lane)] = revl[(size_t)(rptr[(size_t)q] + u)];
-                }
-            }
-            rch.push_back(make_int4((int)s0, (int)(np | ((int64_t)lg << 16)), (int)base, (int)nslots));
-            s0 += np;
-        }
-    }
-    if (rev.empty()) rev.push_back(kRevNone);
-    g.n_fwd_chunks = (int)fch.size();
-    g.n_rev_chunks = (int)rch.size();
+    PackedGraph pk;
+    const bool relabel = !std::getenv("GGP_TREE_ORDER");
+    if (int rc = pack_graph(coords, nbrs, offs, n_off, indices, n0, k, N, D, relabel, &pk, &err))
+        return bail(fail(rc, err));
+    g.n_fwd_chunks = (int)pk.fwd.size();
+    g.n_rev_chunks = (int)pk.revc.size();
     g.sweep_wgs = h->ncu;
     if (const char* e = std::getenv("GGP_SWEEP_WGS_PER_CU")) g.sweep_wgs = h->ncu * std::max(1, atoi(e));
-    // original position of each internal position
-    std::vector<int32_t> idx32;
-    if (indices || relabel) {
-        idx32.resize((size_t)N);
-        for (int64_t i = 0; i < N; ++i)
-            idx32[(size_t)i] = indices ? (int32_t)indices[i2t[(size_t)i]] : i2t[(size_t)i];
-    }
-    std::vector<uint32_t> coords_int((size_t)(N * D));
-    for (int64_t i = 0; i < N; ++i)
-        for (int d = 0; d < D; ++d)
-            coords_int[(size_t)(i * D + d)] = coords[(int64_t)i2t[(size_t)i] * D + d];
-    std::vector<int32_t> i2tm((size_t)std::max<int64_t>(M, 1));
-    for (int64_t m = 0; m < M; ++m) i2tm[(size_t)m] = i2t[(size_t)(n0 + m)] - (int32_t)n0;
     int rc = 0;
     rc |= dmalloc(h, (void**)&g.coords, (size_t)(N * D) * 4);
-    rc |= dmalloc(h, (void**)&g.nbr, nsoa.size() * 4);
-    rc |= dmalloc(h, (void**)&g.rcnt, rcnt.size() * 4);
-    rc |= dmalloc(h, (void**)&g.rev, rev.size() * 4);
-    if (!idx32.empty()) rc |= dmalloc(h, (void**)&g.idx, (size_t)N * 4);
-    if (relabel) {
+    rc |= dmalloc(h, (void**)&g.nbr, pk.nsoa.size() * 4);
+    rc |= dmalloc(h, (void**)&g.rcnt, pk.rcnt.size() * 4);
+    rc |= dmalloc(h, (void**)&g.rev, pk.rev.size() * 4);
+    if (!pk.idx32.empty()) rc |= dmalloc(h, (void**)&g.idx, (size_t)N * 4);
+    if (pk.relabel) {
         rc |= dmalloc(h, (void**)&g.i2t, (size_t)N * 4);
-        rc |= dmalloc(h, (void**)&g.i2tm, i2tm.size() * 4);
+        rc |= dmalloc(h, (void**)&g.i2tm, pk.i2tm.size() * 4);
     }
     rc |= dmalloc(h, &h->mv, (size_t)(M * k) * es);
     rc |= dmalloc(h, &h->sd, (size_t)M * es);
@@ -1029,8 +937,8 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     rc |= dmalloc(h, (void**)&h->scal_partial, std::max(h->nblk_factor, h->nblk_pull) * 8);
     rc |= dmalloc(h, &h->dstat, kStatBytes);
     rc |= dmalloc(h, (void**)&h->dsync, (size_t)dense_sync_ints((int)n0) * sizeof(int));
-    rc |= dmalloc(h, (void**)&g.fwd_chunks, std::max<size_t>(fch.size(), 1) * sizeof(int4));
-    rc |= dmalloc(h, (void**)&g.rev_chunks, std::max<size_t>(rch.size(), 1) * sizeof(int4));
+    rc |= dmalloc(h, (void**)&g.fwd_chunks, std::max<size_t>(pk.fwd.size(), 1) * sizeof(int4));
+    rc |= dmalloc(h, (void**)&g.rev_chunks, std::max<size_t>(pk.revc.size(), 1) * sizeof(int4));
     rc |= dmalloc(h, (void**)&g.sweep_ticket, 16);
     if (rc) return bail(GGP_ERR_HIP);
     if (hipHostMalloc(&h->hstat, kStatBytes) != hipSuccess)
@@ -1041,15 +949,18 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     h->hscal = static_cast<double*>(h->hstat);
     h->hinfo = reinterpret_cast<int*>(static_cast<char*>(h->hstat) + 64);
     h->herr = reinterpret_cast<int*>(static_cast<char*>(h->hstat) + 80);
-    if (hipMemcpy(g.coords, coords_int.data(), (size_t)(N * D) * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        (relabel && hipMemcpy(g.i2t, i2t.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess) ||
-        (relabel && hipMemcpy(g.i2tm, i2tm.data(), i2tm.size() * 4, hipMemcpyHostToDevice) != hipSuccess) ||
-        hipMemcpy(g.nbr, nsoa.data(), nsoa.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(g.rcnt, rcnt.data(), rcnt.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(g.rev, rev.data(), rev.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        (!idx32.empty() && hipMemcpy(g.idx, idx32.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess) ||
-        (!fch.empty() && hipMemcpy(g.fwd_chunks, fch.data(), fch.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess) ||
-        (!rch.empty() && hipMemcpy(g.rev_chunks, rch.data(), rch.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess) ||
+    static_assert(sizeof(Chunk) == sizeof(int4), "a sweep chunk is uploaded as an int4");
+    static_assert(kPackBlock == kBlock && kPackRevSlots == kRevSlots && kPackRevNone == kRevNone,
+                  "the packed layout is the sweep kernels' layout");
+    if (hipMemcpy(g.coords, pk.coords.data(), (size_t)(N * D) * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        (pk.relabel && hipMemcpy(g.i2t, pk.i2t.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess) ||
+        (pk.relabel && hipMemcpy(g.i2tm, pk.i2tm.data(), pk.i2tm.size() * 4, hipMemcpyHostToDevice) != hipSuccess) ||
+        hipMemcpy(g.nbr, pk.nsoa.data(), pk.nsoa.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(g.rcnt, pk.rcnt.data(), pk.rcnt.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(g.rev, pk.rev.data(), pk.rev.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        (!pk.idx32.empty() && hipMemcpy(g.idx, pk.idx32.data(), (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess) ||
+        (!pk.fwd.empty() && hipMemcpy(g.fwd_chunks, pk.fwd.data(), pk.fwd.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess) ||
+        (!pk.revc.empty() && hipMemcpy(g.rev_chunks, pk.revc.data(), pk.revc.size() * sizeof(int4), hipMemcpyHostToDevice) != hipSuccess) ||
         hipMemset(g.sweep_err, 0, 16) != hipSuccess)
         return bail(fail(GGP_ERR_HIP, "hipMemcpy of the graph failed"));
     if (hipStreamCreateWithFlags(&h->s_main, hipStreamNonBlocking) != hipSuccess ||

@@ -30,7 +30,8 @@ namespace ggp {
 namespace {
 
 constexpr int kCompatMaxBlocks = 2048;  // workgroups of the factor launch (partial sums)
-constexpr int kCompatMaxCells = 4096;   // cells of the O(1) segment index
+constexpr int kCompatMaxCells = 4096;   // cells of the O(1) segment index in LDS
+constexpr int kCompatMinLdsCells = 512;  // fewer: the table stays in global memory
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -40,15 +41,19 @@ struct CompatLayout {
     int ucells_max;
 };
 
-// Largest LDS a workgroup of this library uses (the handle path's budget) and the cell count
-// that leaves room for the table in it, as ggp_set_cov_iso chooses.
+// The cell count of the O(1) index as ggp_set_cov_iso chooses it: what the LDS budget leaves
+// beside the table (and a histogram), or, when that is too little, a table in global memory
+// (*global set) with a finer index there.
 template <typename T>
-int cells_for(int64_t nb, size_t lds_max) {
+int cells_for(int64_t nb, size_t lds_max, bool* global) {
     const size_t entb = (size_t)(nb - 1) * sizeof(TabEnt<T>);
     const size_t slack = 512 + (size_t)kWideBlock / 64 * 2 * 64 * sizeof(T);
     const size_t hist = (size_t)nb * 8;
     const size_t budget = lds_max > entb + hist + slack ? lds_max - entb - hist - slack : 0;
-    return (int)std::min<int64_t>(kCompatMaxCells, (int64_t)(budget / 2) - 1);
+    const int64_t cells = std::min<int64_t>(kCompatMaxCells, (int64_t)(budget / 2) - 1);
+    *global = cells < kCompatMinLdsCells;
+    if (*global) return (int)std::min<int64_t>(65536, std::max<int64_t>(4096, 4 * nb));
+    return (int)cells;
 }
 
 template <typename T>
@@ -205,12 +210,9 @@ unsigned factor_blocks(int64_t M, int64_t k, int ncu) {
 
 // Scratch bytes one call needs (0 on a rejected argument, with the error set).
 template <typename T>
-size_t scratch_bytes(const CompatArgs& a, const DevInfo& d, int* cells_out, unsigned* nblk_out) {
-    const int cells = cells_for<T>(a.nb, d.lds);
-    if (cells < 1) {
-        set_error(GGP_ERR_ARG, "covariance table too large for LDS");
-        return 0;
-    }
+size_t scratch_bytes(const CompatArgs& a, const DevInfo& d, int* cells_out, unsigned* nblk_out,
+                     bool* global) {
+    const int cells = cells_for<T>(a.nb, d.lds, global);
     const unsigned nblk = factor_blocks(a.N - a.n0, a.k, d.ncu);
     *cells_out = cells;
     *nblk_out = nblk;
@@ -221,9 +223,10 @@ size_t scratch_bytes(const CompatArgs& a, const DevInfo& d, int* cells_out, unsi
 // stream `st`, using `scratch` (at least scratch_bytes bytes).
 template <typename T>
 int enqueue(const CompatArgs& a, int op, unsigned char* scratch, int cells, unsigned nblk,
-            hipStream_t st) {
+            bool global, hipStream_t st) {
     const CompatLayout<T> L = layout<T>(a.nb, cells, (int)nblk);
     Table<T> tb;
+    tb.global = global;
     tb.params = reinterpret_cast<TabParams<T>*>(scratch);
     tb.tab = reinterpret_cast<TabEnt<T>*>(scratch + L.tab);
     tb.acc = reinterpret_cast<uint16_t*>(scratch + L.acc);
@@ -297,14 +300,14 @@ int run_noalloc(const CompatArgs& a, int op, hipStream_t st) {
     if (int rc = dev_info(d)) return rc;
     int cells = 0;
     unsigned nblk = 0;
-    const size_t bytes = scratch_bytes<T>(a, d, &cells, &nblk);
-    if (!bytes) return GGP_ERR_ARG;
+    bool global = false;
+    const size_t bytes = scratch_bytes<T>(a, d, &cells, &nblk, &global);
     if (bytes > kNoAllocBytes)
         return set_error(GGP_ERR_ARG, "problem needs more scratch than the allocation-free entry "
                                       "point's fixed 64 KiB");
     unsigned char* p = nullptr;
     if (int rc = scratch_of_device(&p)) return rc;
-    return enqueue<T>(a, op, p, cells, nblk, st);
+    return enqueue<T>(a, op, p, cells, nblk, global, st);
 }
 
 template <typename T>
@@ -314,12 +317,12 @@ int run_alloc(const CompatArgs& a, int op, hipStream_t st) {
     if (int rc = dev_info(d)) return rc;
     int cells = 0;
     unsigned nblk = 0;
-    const size_t bytes = scratch_bytes<T>(a, d, &cells, &nblk);
-    if (!bytes) return GGP_ERR_ARG;
+    bool global = false;
+    const size_t bytes = scratch_bytes<T>(a, d, &cells, &nblk, &global);
     void* p = nullptr;
     hipError_t e = hipMallocAsync(&p, bytes, st);
     if (e != hipSuccess) return set_error(GGP_ERR_HIP, std::string("hipMallocAsync: ") + hipGetErrorString(e));
-    const int rc = enqueue<T>(a, op, static_cast<unsigned char*>(p), cells, nblk, st);
+    const int rc = enqueue<T>(a, op, static_cast<unsigned char*>(p), cells, nblk, global, st);
     e = hipFreeAsync(p, st);
     if (rc) return rc;
     if (e != hipSuccess) return set_error(GGP_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(e));

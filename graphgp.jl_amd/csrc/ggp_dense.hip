@@ -269,13 +269,20 @@ __device__ inline void walk_accumulate(T (&acc)[4], const T* A, int n, int nt, i
     }
 }
 
+// Whether the walker factor of the element type takes one reciprocal square root per column
+// (pivot * rsq, within 1 ulp) instead of sqrt and a division. Off for both types: with sqrt and
+// the IEEE division every entry of the factor carries the unblocked recurrence's bits, so the
+// factor equals the oracle's (and the Float32 dense-layer cotangents, which amplify the
+// factor's rounding through L^-1, agree with the oracle's to the rounding of their own sums).
+template <typename T> constexpr bool kRsqFactor = false;
+
 // Solve the tile in sA against L (row r on lane r of wave 0) into global tile (i, j) and, if
 // out is given, into out (LDS). Called by wave 0.
 template <typename T>
 __device__ inline void walk_solve(T* A, int n, int i, int j, const T (*sA)[kTile + 1],
                                   const T (*L)[kTile + 1], const T* inv, T (*out)[kTile + 1],
                                   int tid) {
-    constexpr bool kRsq = std::is_same<T, float>::value;
+    constexpr bool kRsq = kRsqFactor<T>;
     const int r = tid & (kTile - 1);
     const bool live = tid < kTile && i * kTile + r < n;
     T a[kTile];
@@ -316,16 +323,16 @@ __host__ __device__ inline int dense_sync_flag_ints(int nt) { return (nt * nt + 
 // fma(-L[r][p], L[c][p], .) when p < c, and fma(-L[r][p], 0, .) (no change) otherwise, so each
 // entry keeps the unblocked left-looking chain in its order. Entries above the diagonal are
 // scratch (updated, never stored).
-// f64: L[p][p] = sqrt(pivot) and the column divided by it (the oracle's bits). f32: one
-// reciprocal square root per column (v_rsq_f32, within 1 ulp): L[p][p] = pivot * rsq and the
-// column multiplied by rsq, which takes the square root and the division off the
-// column-to-column chain; rsq goes to inv (LDS) and dinv (global, for the helpers' solves).
+// L[p][p] = sqrt(pivot) and the column divided by it (the oracle's bits). With kRsqFactor (off):
+// one reciprocal square root per column (v_rsq_f32, within 1 ulp), L[p][p] = pivot * rsq and
+// the column multiplied by rsq, which takes the square root and the division off the
+// column-to-column chain; rsq then goes to inv (LDS) and dinv (global, for the helpers' solves).
 // Called by wave 0.
 template <typename T>
 __device__ inline void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1],
                                      T (*Lt)[kLtPitch], T* inv, T* dinv, T (*col)[kTile],
                                      int tid, int* info) {
-    constexpr bool kRsq = std::is_same<T, float>::value;
+    constexpr bool kRsq = kRsqFactor<T>;
     const int r = tid & (kTile - 1), h = tid >> 5;
     const bool live = j * kTile + r < n;
     T a[16];
@@ -384,7 +391,7 @@ template <typename T>
 __device__ inline void walk_solve_t(T* A, int n, int i, int j, const T (*sC)[kTile + 1],
                                     const T (*Lt)[kLtPitch], const T* inv, T (*P)[kTile + 1],
                                     int tid) {
-    constexpr bool kRsq = std::is_same<T, float>::value;
+    constexpr bool kRsq = kRsqFactor<T>;
     const int r = tid & (kTile - 1), h = tid >> 5;
     T a[16];
 #pragma unroll
@@ -549,7 +556,7 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, in
                 sA[r][c] = acc[q];
                 sB[r][c] = (g * kTile + r < n && c <= r) ? A[(int64_t)(g * kTile + r) * n + g * kTile + c] : T(0);
             }
-            if (std::is_same<T, float>::value && tid < kTile)
+            if (kRsqFactor<T> && tid < kTile)
                 sInv[tid] = g * kTile + tid < n ? dinv[g * kTile + tid] : T(1);
             __syncthreads();
             if (tid < 64) walk_solve(A, n, i, g, sA, sB, sInv, (T(*)[kTile + 1])nullptr, tid);
@@ -1085,8 +1092,9 @@ enum DenseMode { DM_LOGDET = 0, DM_GENERATE = 1, DM_INVLOSS = 2 };
 // Scatter the dense covariance cotangent through the lookup weights (src/dense.jl:166-181,
 // 244-252; src/grad_generate_vals.jl:196-211). Pairs (a >= b) of the lower triangle are split
 // over the grid; each workgroup accumulates an f64 LDS histogram and writes it to its row of
-// hist_partial.
-template <typename T, int D, int MODE>
+// hist_partial. HG (a table too large for LDS): the workgroup accumulates with f64 atomics
+// directly in its row, which the host zeroes before the launch.
+template <typename T, int D, int MODE, bool HG>
 __global__ void __launch_bounds__(256) k_dense_scatter(const uint32_t* __restrict__ coords,
                                                        int n, T scale,
                                                        const TabEnt<T>* __restrict__ tab,
@@ -1096,9 +1104,12 @@ __global__ void __launch_bounds__(256) k_dense_scatter(const uint32_t* __restric
                                                        const T* __restrict__ alpha,
                                                        double* __restrict__ hist_partial) {
     const TabParams<T> P = *Pp;
-    extern __shared__ double s_hist[];
-    for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
-    __syncthreads();
+    extern __shared__ double s_lds_hist[];
+    double* s_hist = HG ? hist_partial + (size_t)blockIdx.x * P.nb : s_lds_hist;
+    if (!HG) {
+        for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
+        __syncthreads();
+    }
     const int64_t npairs = (int64_t)n * (n + 1) / 2;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < npairs; t += stride) {
@@ -1129,13 +1140,17 @@ __global__ void __launch_bounds__(256) k_dense_scatter(const uint32_t* __restric
         atomicAdd(&s_hist[lo], gv * (double)wlo);
         atomicAdd(&s_hist[lo + 1], gv * (double)whi);
     }
-    __syncthreads();
-    double* out = hist_partial + (size_t)blockIdx.x * P.nb;
-    for (int i = threadIdx.x; i < P.nb; i += blockDim.x) out[i] = s_hist[i];
+    if (!HG) {
+        __syncthreads();
+        double* out = hist_partial + (size_t)blockIdx.x * P.nb;
+        for (int i = threadIdx.x; i < P.nb; i += blockDim.x) out[i] = s_hist[i];
+    }
 }
 
 template <typename T>
-size_t dense_scatter_lds(const Table<T>& tb) { return (size_t)tb.P.nb * sizeof(double); }
+size_t dense_scatter_lds(const Table<T>& tb) {
+    return tb.global ? 0 : (size_t)tb.P.nb * sizeof(double);
+}
 
 template <typename T, int MODE>
 static void launch_dense_scatter(const Graph& g, const Table<T>& tb, const double* C,
@@ -1143,12 +1158,23 @@ static void launch_dense_scatter(const Graph& g, const Table<T>& tb, const doubl
     const size_t lds = dense_scatter_lds(tb);
     const int n = (int)g.n0;
     const T scale = (T)g.scale;
+    if (tb.global) launch_fill<double>(hist_partial, 0.0, (int64_t)nw * tb.P.nb, st);
+#define GGP_SCAT(DD, HG)                                                                       \
+    hipLaunchKernelGGL((k_dense_scatter<T, DD, MODE, HG>), dim3(nw), dim3(256), lds, st,        \
+                       g.coords, n, scale, tb.tab, tb.acc, tb.params, C, alpha, hist_partial)
+#define GGP_SCAT_D(DD)                                                                         \
+    do {                                                                                       \
+        if (tb.global) GGP_SCAT(DD, true);                                                     \
+        else GGP_SCAT(DD, false);                                                              \
+    } while (0)
     switch (g.D) {
-        case 2: hipLaunchKernelGGL((k_dense_scatter<T, 2, MODE>), dim3(nw), dim3(256), lds, st, g.coords, n, scale, tb.tab, tb.acc, tb.params, C, alpha, hist_partial); break;
-        case 3: hipLaunchKernelGGL((k_dense_scatter<T, 3, MODE>), dim3(nw), dim3(256), lds, st, g.coords, n, scale, tb.tab, tb.acc, tb.params, C, alpha, hist_partial); break;
-        case 4: hipLaunchKernelGGL((k_dense_scatter<T, 4, MODE>), dim3(nw), dim3(256), lds, st, g.coords, n, scale, tb.tab, tb.acc, tb.params, C, alpha, hist_partial); break;
+        case 2: GGP_SCAT_D(2); break;
+        case 3: GGP_SCAT_D(3); break;
+        case 4: GGP_SCAT_D(4); break;
         default: break;
     }
+#undef GGP_SCAT_D
+#undef GGP_SCAT
 }
 
 

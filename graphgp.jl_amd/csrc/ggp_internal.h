@@ -59,6 +59,11 @@ struct Table {
     TabParams<T>* params = nullptr;  // device copy of P
     uint16_t* acc = nullptr;    // ucells+1 entries
     TabParams<T> P{};
+    // The table (entries + cell index) and the d/dvals histogram do not fit the LDS budget: the
+    // per-point kernels then read the table from global memory and accumulate the histogram
+    // with f64 atomics into their own global row (every k runs on the wavefront-per-point
+    // kernels, which have this form).
+    bool global = false;
     std::vector<T> bins, vals;  // host copies
     AnisoArgs<T> aniso{};        // device arrays of the anisotropic table (grid == null: isotropic)
     std::vector<T> aniso_host;   // host copy: [sb, zb, grid]
@@ -112,6 +117,19 @@ struct WideD {
                          const T* vb, double* hist_partial, double* scalar_partial,
                          unsigned nblk, hipStream_t st);
 };
+// The pullback with the table in global memory (ggp_wide.hip, part 2), behind WideD.
+template <typename T, int D>
+struct WideG {
+    static void pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, const T* xi,
+                         const T* vb, double* hist_partial, double* scalar_partial,
+                         unsigned nblk, hipStream_t st);
+};
+extern template struct WideG<float, 2>;
+extern template struct WideG<float, 3>;
+extern template struct WideG<float, 4>;
+extern template struct WideG<double, 2>;
+extern template struct WideG<double, 3>;
+extern template struct WideG<double, 4>;
 extern template struct WideD<float, 2>;
 extern template struct WideD<float, 3>;
 extern template struct WideD<float, 4>;

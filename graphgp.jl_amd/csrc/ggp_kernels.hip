@@ -147,11 +147,14 @@ template <typename T, int K> using Launch = typename LaunchSel<T, K>::type;
         }                                            \
     } while (0)
 
+// A table in global memory (too large for LDS) runs on the wavefront-per-point kernels for
+// every k: they have the global-table form, and give the same IEEE results.
 template <typename T>
 void launch_factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
                    double* partial, const T* values, T* xi_out, unsigned nblk, hipStream_t st) {
 #define CALLF(KK) Launch<T, KK>::factor(g, tb, mode, mv, sd, terms, partial, values, xi_out, nblk, st)
-    GGP_FOR_K(CALLF);
+    if (tb.global) CALLF(0);
+    else GGP_FOR_K(CALLF);
 #undef CALLF
 }
 
@@ -160,7 +163,8 @@ void launch_pullback(const Graph& g, const Table<T>& tb, int mode, const T* v, c
                      const T* vb, double* hist_partial, double* scalar_partial, unsigned nblk,
                      hipStream_t st) {
 #define CALLP(KK) Launch<T, KK>::pullback(g, tb, mode, v, xi, vb, hist_partial, scalar_partial, nblk, st)
-    GGP_FOR_K(CALLP);
+    if (tb.global) CALLP(0);
+    else GGP_FOR_K(CALLP);
 #undef CALLP
 }
 

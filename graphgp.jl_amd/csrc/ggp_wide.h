@@ -143,14 +143,18 @@ __device__ inline T wide_mean_vec(const T (&a)[kWideN], int K, int lane) {
 }
 
 // ---- factor pass (k_factor's twin) ----------------------------------------------------------
-template <typename T, int D, int MODE, bool ANISO>
+// TG: the table is read from global memory (too large for LDS) instead of being staged. MODE = -1:
+// the mode is the run-time rt_mode (one instantiation serves every mode; used for TG, whose
+// speed matters less than its build time).
+template <typename T, int D, int MODE, bool ANISO, bool TG>
 __global__ void __launch_bounds__(kWideBlock)
 k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, int64_t M,
            int64_t n0, int K, T scale, const TabEnt<T>* __restrict__ g_tab,
            const uint16_t* __restrict__ g_acc, const TabParams<T>* __restrict__ Pp,
            T* __restrict__ mv, T* __restrict__ sd, T* __restrict__ terms,
            double* __restrict__ partial, const T* __restrict__ values, T* __restrict__ xi_out,
-           AnisoArgs<T> an, const int64_t* __restrict__ nbr64) {
+           AnisoArgs<T> an, const int64_t* __restrict__ nbr64, int rt_mode) {
+    const int mode = MODE >= 0 ? MODE : rt_mode;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ double s_red[kWideWaves];
     TabParams<T> P{};
@@ -158,9 +162,14 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
     uint16_t* s_acc = nullptr;
     if (!ANISO) {
         P = *Pp;
-        s_tab = reinterpret_cast<TabEnt<T>*>(smem);
-        s_acc = reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
-        stage_table(s_tab, s_acc, g_tab, g_acc, P);
+        if (TG) {
+            s_tab = const_cast<TabEnt<T>*>(g_tab);
+            s_acc = const_cast<uint16_t*>(g_acc);
+        } else {
+            s_tab = reinterpret_cast<TabEnt<T>*>(smem);
+            s_acc = reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
+            stage_table(s_tab, s_acc, g_tab, g_acc, P);
+        }
     }
     const int lane = threadIdx.x & 63;
     const int n = K + 1;
@@ -172,20 +181,20 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
         T a[kWideN], unused[kWideN];
         wide_assemble<T, D, ANISO>(a, x, n, lane, scale, s_tab, s_acc, P, an);
         const T s = wide_cholesky<T, false>(a, unused, n, K, lane);
-        if (MODE & F_TERMS) {
+        if (mode & F_TERMS) {
             const T t = num<T>::log(s);
             if (lane == 0) {
                 if (terms) terms[m] = t;
                 lsum += (double)t;
             }
         }
-        if (MODE & (F_MV | F_INV)) {
+        if (mode & (F_MV | F_INV)) {
             const T xm = wide_mean_vec(a, K, lane);
-            if (MODE & F_MV) {
+            if (mode & F_MV) {
                 if (lane < K) mv[m * K + lane] = xm;
                 if (lane == 0) sd[m] = s;
             }
-            if (MODE & F_INV) {  // src/kernels.jl:48-55
+            if (mode & F_INV) {  // src/kernels.jl:48-55
                 const T prod = lane < K ? xm * values[nb] : T(0);
                 T mean = T(0);
 #pragma unroll
@@ -195,32 +204,41 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
             }
         }
     }
-    if (MODE & F_TERMS) {
+    if (mode & F_TERMS) {
         const double t = block_sum(lsum, s_red);
         if (threadIdx.x == 0) partial[blockIdx.x] = t;
     }
 }
 
 // ---- adjoint pullback (k_pullback's twin) ---------------------------------------------------
-template <typename T, int D, int MODE>
+// TG: the table is read from global memory and the histogram is accumulated with f64 atomics
+// directly in this workgroup's row of hist_partial (zeroed by the host before the launch).
+// MODE = -1: the mode is the run-time rt_mode (as for k_factor_w).
+template <typename T, int D, int MODE, bool TG>
 __global__ void __launch_bounds__(kWideBlock)
 k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, int64_t M,
              int64_t n0, int K, T scale, const TabEnt<T>* __restrict__ g_tab,
              const uint16_t* __restrict__ g_acc, const TabParams<T>* __restrict__ Pp,
              const T* __restrict__ v, const T* __restrict__ xi, const T* __restrict__ vb,
-             double* __restrict__ hist_partial, double* __restrict__ scalar_partial) {
-    constexpr int SEED = MODE & 3;
-    constexpr bool PTS = (MODE & P_PTS) != 0;
+             double* __restrict__ hist_partial, double* __restrict__ scalar_partial,
+             int rt_mode) {
+    const int mode = MODE >= 0 ? MODE : rt_mode;
+    const int SEED = mode & 3;
+    const bool PTS = (mode & P_PTS) != 0;
     const TabParams<T> P = *Pp;
     extern __shared__ __align__(16) unsigned char smem[];
-    TabEnt<T>* s_tab = reinterpret_cast<TabEnt<T>*>(smem);
-    uint16_t* s_acc = reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
-    double* s_hist = reinterpret_cast<double*>(smem + tab_bytes<T>(P.nb, P.ucells));
+    TabEnt<T>* s_tab = TG ? const_cast<TabEnt<T>*>(g_tab) : reinterpret_cast<TabEnt<T>*>(smem);
+    uint16_t* s_acc = TG ? const_cast<uint16_t*>(g_acc)
+                         : reinterpret_cast<uint16_t*>(smem + (size_t)(P.nb - 1) * sizeof(TabEnt<T>));
+    double* s_hist = TG ? hist_partial + (size_t)blockIdx.x * P.nb
+                        : reinterpret_cast<double*>(smem + tab_bytes<T>(P.nb, P.ucells));
     __shared__ double s_red[kWideWaves];
     __shared__ T s_xch[kWideWaves][2][64];
-    if (!PTS)
-        for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
-    stage_table(s_tab, s_acc, g_tab, g_acc, P);
+    if (!TG) {
+        if (!PTS)
+            for (int i = threadIdx.x; i < P.nb; i += blockDim.x) s_hist[i] = 0.0;
+        stage_table(s_tab, s_acc, g_tab, g_acc, P);
+    }
 
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
@@ -381,7 +399,7 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
         }
     }
     __syncthreads();
-    if (!PTS) {
+    if (!PTS && !TG) {
         double* out = hist_partial + (size_t)blockIdx.x * P.nb;
         for (int i = threadIdx.x; i < P.nb; i += blockDim.x) out[i] = s_hist[i];
     }

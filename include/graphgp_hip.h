@@ -235,7 +235,8 @@ int ggp_build_graph_device(const double* points, int64_t N, int32_t D, int64_t n
 /* ---- measurement ------------------------------------------------------------------------- */
 /* No counterpart in the reference (its benchmarks time whole calls, bench/compare/run_julia.jl:50-58).
  * `enable` is a bit mask over "factor" (1), "pullback" (2), "sweep_fwd" (4), "sweep_rev" (8),
- * "dense" (16) and "op" (32, the whole op); 0 turns timing off, 63 times everything. Each
+ * "dense" (16: assembly + Cholesky of the dense block), "op" (32, the whole op) and "potrf"
+ * (64: the dense Cholesky launch alone); 0 turns timing off, 127 times everything. Each
  * enabled timer brackets its kernels with HIP events on the stream they run on (every event
  * pair adds a few microseconds to the op); ggp_kernel_timer_read returns the summed
  * milliseconds and the number of timed launches for one name. Enabling resets the sums. */

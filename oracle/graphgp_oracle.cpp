@@ -56,9 +56,13 @@ struct Prob {
     const void* grid;   // ns x nz, row-major: grid[i*nz + j] = K(sbins[i], zbins[j])
     int64_t ns, nz;
     double alpha;
-    // Accumulate the d/dvals histograms in double instead of T. The reference sums in T
-    // (src/grad.jl:32-87), so the default mirrors it; the double mode removes the summation
-    // noise of very large point sets from comparisons whose subject is the per-point arithmetic.
+    // Accumulate the d/dvals histograms in double instead of T, and evaluate the dense-layer
+    // cotangents (the n0 x n0 Cholesky adjoint, K^-1, alpha) in double from the T factor. The
+    // reference sums and evaluates both in T (src/grad.jl:32-87, src/dense.jl:153-252,
+    // src/grad_generate_vals.jl:188-211), so the default mirrors it; the double mode removes
+    // the rounding noise of very large point sets and of the O(n0^3) dense loops in T from
+    // comparisons whose subject is the per-point arithmetic (the library evaluates the dense
+    // cotangents in double).
     int acc64;
 };
 
@@ -552,6 +556,56 @@ void dense_scatter(const Prob& p, int64_t n, const T* G, T* dv) {
         }
 }
 
+// dense_scatter with a double cotangent and double accumulation (radii and weights in T, as
+// the reference computes them).
+template <typename T>
+void dense_scatter64(const Prob& p, int64_t n, const double* G, double* dv) {
+    const T* bins = (const T*)p.bins; const T scale = T(p.scale);
+    const int64_t D = p.D;
+    for (int64_t b = 0; b < n; ++b)
+        for (int64_t a = b; a < n; ++a) {
+            int64_t sq = sqdist(p.coords + a * D, p.coords + b * D, D);
+            T r = std::sqrt(T(sq)) * scale;
+            int64_t lo; T wlo, whi;
+            cov_lookup_weights(r, bins, p.nbins, lo, wlo, whi);
+            const double g = G[a * n + b];
+            dv[lo] += g * (double)wlo;
+            dv[lo + 1] += g * (double)whi;
+        }
+}
+
+// The dense logdet and inverse-loss cotangents of src/dense.jl:153-183 / 229-252 in double,
+// from the T factor (the acc64 mode).
+template <typename T>
+void dense_logdet_grad_vals64(const Prob& p, const std::vector<T>& L, double* dv) {
+    const int64_t n = p.n0;
+    std::vector<double> Ld(L.begin(), L.end()), Linv(n * n, 0.0), e(n), col(n), G(n * n, 0.0);
+    for (int64_t c = 0; c < n; ++c) {
+        for (int64_t i = 0; i < n; ++i) e[i] = i == c ? 1.0 : 0.0;
+        trsv_lower(Ld.data(), n, e.data(), col.data());
+        for (int64_t i = 0; i < n; ++i) Linv[i * n + c] = col[i];
+    }
+    for (int64_t b = 0; b < n; ++b)
+        for (int64_t a = b; a < n; ++a) {
+            double kinv = 0.0;
+            for (int64_t kk = 0; kk < n; ++kk) kinv += Linv[kk * n + a] * Linv[kk * n + b];
+            G[a * n + b] = a == b ? 0.5 * kinv : kinv;
+        }
+    dense_scatter64<T>(p, n, G.data(), dv);
+}
+template <typename T>
+void dense_inv_loss_grad_vals64(const Prob& p, const std::vector<T>& L, const T* y, double* dv,
+                                double* xi_out) {
+    const int64_t n = p.n0;
+    std::vector<double> Ld(L.begin(), L.end()), yd(y, y + n), alpha(n), G(n * n, 0.0);
+    trsv_lower(Ld.data(), n, yd.data(), xi_out);
+    trsv_lower_t(Ld.data(), n, xi_out, alpha.data());
+    for (int64_t b = 0; b < n; ++b)
+        for (int64_t a = b; a < n; ++a)
+            G[a * n + b] = a == b ? -0.5 * alpha[a] * alpha[a] : -alpha[a] * alpha[b];
+    dense_scatter64<T>(p, n, G.data(), dv);
+}
+
 // ---- src/dense.jl:153-183 -------------------------------------------------------------------
 template <typename T>
 void dense_logdet_grad_vals(const Prob& p, const std::vector<T>& L, T* dv) {
@@ -683,9 +737,15 @@ int generate_logdet_grad_vals(const Prob& p, T* dvals, double* logdet) {
     refine_logdet_grad_vals(p, dvals, &ld_ref);
     std::vector<T> L;
     if (!dense_factor(p, L)) return 6;
-    std::vector<T> dd(p.nbins, T(0));
-    dense_logdet_grad_vals(p, L, dd.data());
-    for (int64_t i = 0; i < p.nbins; ++i) dvals[i] = dd[i] + dvals[i];
+    if (p.acc64) {
+        std::vector<double> dd(p.nbins, 0.0);
+        dense_logdet_grad_vals64(p, L, dd.data());
+        for (int64_t i = 0; i < p.nbins; ++i) dvals[i] = (T)(dd[i] + (double)dvals[i]);
+    } else {
+        std::vector<T> dd(p.nbins, T(0));
+        dense_logdet_grad_vals(p, L, dd.data());
+        for (int64_t i = 0; i < p.nbins; ++i) dvals[i] = dd[i] + dvals[i];
+    }
     T ld_dense = T(0);
     for (int64_t i = 0; i < p.n0; ++i) ld_dense += std::log(L[i * p.n0 + i]);
     if (logdet) *logdet = (double)(ld_dense + (T)ld_ref);
@@ -768,12 +828,22 @@ int generate_inv_loss_grad_vals(const Prob& p, const T* data, T* dvals, double* 
     for (int64_t i = 0; i < N; ++i) d[i] = p.indices ? data[p.indices[i]] : data[i];
     std::vector<T> L;
     if (!dense_factor(p, L)) return 6;
+    double ref_loss = 0;
+    if (p.acc64) {
+        std::vector<double> xid(n0), gd(p.nbins, 0.0);
+        dense_inv_loss_grad_vals64(p, L, d.data(), gd.data(), xid.data());
+        double dense_loss = 0.0;
+        for (int64_t i = 0; i < n0; ++i) dense_loss += xid[i] * xid[i];
+        refine_inv_loss_grad_vals(p, d.data(), dvals, &ref_loss);
+        for (int64_t i = 0; i < p.nbins; ++i) dvals[i] = (T)((double)dvals[i] + gd[i]);
+        if (loss) *loss = dense_loss / 2.0 + ref_loss;
+        return 0;
+    }
     std::vector<T> xid(n0), gd(p.nbins, T(0));
     dense_inv_loss_grad_vals(p, L, d.data(), gd.data(), xid.data());
     T dense_loss = T(0);
     for (int64_t i = 0; i < n0; ++i) dense_loss += xid[i] * xid[i];
     dense_loss = dense_loss / T(2);
-    double ref_loss = 0;
     refine_inv_loss_grad_vals(p, d.data(), dvals, &ref_loss);
     for (int64_t i = 0; i < p.nbins; ++i) dvals[i] = dvals[i] + gd[i];
     if (loss) *loss = (double)(dense_loss + (T)ref_loss);
@@ -874,7 +944,29 @@ int generate_grad_vals(const Prob& p, const T* xi, const T* vbar, T* dvals) {
                 if (nbj >= 0) vb[nbj] += mv[m * K + j] * vbp;
             }
         }
-    // Dense backward (grad_generate_vals.jl:188-211).
+    // Dense backward (grad_generate_vals.jl:188-211); with acc64 in double from the T factor.
+    if (p.acc64) {
+        std::vector<double> Ld(L.begin(), L.end()), Lb(n0 * n0, 0.0), Kb(n0 * n0, 0.0);
+        for (int64_t j = 0; j < n0; ++j)
+            for (int64_t i = j; i < n0; ++i) Lb[i * n0 + j] = (double)vb[i] * (double)xih[j];
+        chol_pullback_impl<double, true>(Kb.data(), Lb.data(), Ld.data(), n0);
+        for (int64_t j = 0; j < n0; ++j)
+            for (int64_t i = j + 1; i < n0; ++i) Kb[j * n0 + i] = 0.0;  // lower triangle only
+        for (int64_t j = 0; j < n0; ++j) {
+            dv64[0] += Kb[j * n0 + j];
+            for (int64_t i = j + 1; i < n0; ++i) {
+                int64_t sq = sqdist(p.coords + i * D, p.coords + j * D, D);
+                T r = std::sqrt(T(sq)) * scale;
+                int64_t lo; T wlo, whi;
+                cov_lookup_weights(r, bins, nb, lo, wlo, whi);
+                const double g = Kb[i * n0 + j];
+                dv64[lo] += g * (double)wlo;
+                dv64[lo + 1] += g * (double)whi;
+            }
+        }
+        for (int64_t i = 0; i < nb; ++i) dvals[i] = (T)dv64[i];
+        return 0;
+    }
     std::vector<T> Lbar_d(n0 * n0, T(0)), Kbar_d(n0 * n0, T(0));
     for (int64_t j = 0; j < n0; ++j)
         for (int64_t i = j; i < n0; ++i) Lbar_d[i * n0 + j] = vb[i] * xih[j];

@@ -254,3 +254,34 @@ def test_double_histogram_mode_only_changes_the_summation():
     _, g32 = p32.refine_logdet_grad_vals()
     _, g32d = q32.refine_logdet_grad_vals()
     assert relerr(g32d, g) <= relerr(g32, g) * 1.01 + 1e-7
+
+
+def test_double_mode_dense_cotangents():
+    """acc64 also evaluates the dense-layer cotangents (the Cholesky adjoint of
+    generate_grad_vals, K^-1 of the logdet gradient, alpha of the inverse loss) in double from
+    the factor. In Float64 that is the default's arithmetic: the two modes agree to rounding. In
+    Float32 the double evaluation must sit at least as close to the Float64 answer as the
+    Float32 loops do (it removes their rounding, not the factor's)."""
+    p, z = fixture("generate_parity")
+    q = O.Problem(p.coords, p.neighbors, p.offsets, p.n0, p.scale, p.bins, p.vals,
+                  indices=p.indices, acc64=True)
+    rng = np.random.default_rng(3)
+    xi, vb, d = (rng.standard_normal(p.N) for _ in range(3))
+    assert relerr(q.generate_grad_vals(xi, vb), p.generate_grad_vals(xi, vb)) < 1e-13
+    assert relerr(q.generate_logdet_grad_vals()[1], p.generate_logdet_grad_vals()[1]) < 1e-13
+    l64, g64 = p.generate_inv_loss_grad_vals(d)
+    lq, gq = q.generate_inv_loss_grad_vals(d)
+    assert relerr(gq, g64) < 1e-13 and abs(lq - l64) <= 1e-13 * abs(l64)
+    p32 = p.with_dtype(np.float32)
+    q32 = O.Problem(p32.coords, p32.neighbors, p32.offsets, p32.n0, p32.scale, p32.bins,
+                    p32.vals, indices=p32.indices, dtype=np.float32, acc64=True)
+    x32, v32, d32 = xi.astype(np.float32), vb.astype(np.float32), d.astype(np.float32)
+    want = p.generate_grad_vals(x32.astype(float), v32.astype(float))
+    assert relerr(q32.generate_grad_vals(x32, v32), want) <= \
+        relerr(p32.generate_grad_vals(x32, v32), want) * 1.05 + 1e-7
+    want = p.generate_logdet_grad_vals()[1]
+    assert relerr(q32.generate_logdet_grad_vals()[1], want) <= \
+        relerr(p32.generate_logdet_grad_vals()[1], want) * 1.05 + 1e-7
+    want = p.generate_inv_loss_grad_vals(d32.astype(float))[1]
+    assert relerr(q32.generate_inv_loss_grad_vals(d32)[1], want) <= \
+        relerr(p32.generate_inv_loss_grad_vals(d32)[1], want) * 1.05 + 1e-7
