@@ -69,13 +69,11 @@ __device__ inline int64_t seg_of(const Geom& g, int64_t i) {
 // Segment extents per dimension; split = the first dimension of largest extent. A wavefront
 // covers kChunk positions of one segment; with one chunk per segment it writes the split
 // itself, otherwise per-chunk extents for k_tree_split.
+// One (segment, chunk) task of k_tree_extent on one wavefront.
 template <int D>
-__global__ void __launch_bounds__(kGbBlock)
-k_tree_extent(const double* __restrict__ pts, Geom g, int64_t nseg, int gps,
-              double* __restrict__ pmin, double* __restrict__ pmax, int8_t* __restrict__ split) {
-    const int lane = threadIdx.x & 63;
-    const int64_t w = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    if (w >= nseg * gps) return;  // uniform per wavefront
+__device__ inline void extent_task(const double* __restrict__ pts, const Geom& g, int gps,
+                                   int64_t w, int lane, double* __restrict__ pmin,
+                                   double* __restrict__ pmax, int8_t* __restrict__ split) {
     const int64_t ii = w / gps;
     const int c = (int)(w % gps);
     const int64_t s0 = seg_start(g, ii), end = s0 + seg_size(g, ii);
@@ -116,6 +114,19 @@ k_tree_extent(const double* __restrict__ pts, Geom g, int64_t nseg, int gps,
             pmax[w * D + d] = mx[d];
         }
     }
+}
+
+template <int D>
+__global__ void __launch_bounds__(kGbBlock)
+k_tree_extent(const double* __restrict__ pts, Geom g, int64_t nseg, int gps,
+              double* __restrict__ pmin, double* __restrict__ pmax, int8_t* __restrict__ split) {
+    const int lane = threadIdx.x & 63;
+    // one wavefront per (segment, chunk) task, grid-stride: a deep level of a large build has
+    // more tasks than a launch may hold wavefronts (at most 2^32 work-items per dimension)
+    const int64_t wstride = ((int64_t)gridDim.x * blockDim.x) >> 6;
+    for (int64_t w = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; w < nseg * gps;
+         w += wstride)  // uniform per wavefront
+        extent_task<D>(pts, g, gps, w, lane, pmin, pmax, split);
 }
 
 template <int D>
@@ -364,11 +375,12 @@ __global__ void k_depth_gather(int64_t N, const int32_t* __restrict__ sp,
 
 __global__ void k_nbr_remap(const int32_t* __restrict__ nbr, const int32_t* __restrict__ inv,
                             int64_t n0, int64_t M, int k, int64_t* __restrict__ out) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= M * k) return;
-    const int64_t m_old = t / k, j = t % k;
-    const int64_t m_new = inv[n0 + m_old] - n0;
-    out[m_new * k + j] = inv[nbr[t]];
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;  // M*k may pass 2^32
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < M * k; t += stride) {
+        const int64_t m_old = t / k, j = t % k;
+        const int64_t m_new = inv[n0 + m_old] - n0;
+        out[m_new * k + j] = inv[nbr[t]];
+    }
 }
 
 // ---- 4. lattice and offsets -----------------------------------------------------------------
@@ -415,11 +427,12 @@ struct Origin {
 template <int D>
 __global__ void k_quantize(const double* __restrict__ spts, int64_t N, Origin org, double scale,
                            double lmax, uint32_t* __restrict__ coords) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= N * D) return;
-    const int d = (int)(t % D);
-    const double c = rint((spts[t] - org.o[d]) / scale);
-    coords[t] = (uint32_t)fmin(fmax(c, 0.0), lmax);
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;  // N*D may pass 2^32
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < N * D; t += stride) {
+        const int d = (int)(t % D);
+        const double c = rint((spts[t] - org.o[d]) / scale);
+        coords[t] = (uint32_t)fmin(fmax(c, 0.0), lmax);
+    }
 }
 
 __global__ void k_level_ends(const uint32_t* __restrict__ sdepth, int64_t N,
@@ -430,6 +443,10 @@ __global__ void k_level_ends(const uint32_t* __restrict__ sdepth, int64_t N,
 }
 
 inline unsigned nblocks(int64_t n) { return (unsigned)((n + kGbBlock - 1) / kGbBlock); }
+// Grid of a grid-stride kernel: at most 2^20 workgroups (2^28 work-items).
+inline unsigned nblocks_capped(int64_t n) {
+    return (unsigned)std::min<int64_t>((n + kGbBlock - 1) / kGbBlock, (int64_t)1 << 20);
+}
 
 // ---- the pipeline --------------------------------------------------------------------------
 struct Bufs {
@@ -495,7 +512,7 @@ int build(const double* points, int64_t N, int64_t n0, int k, int lattice_bits, 
         const int64_t n_items = N - g.n_above;
         const int64_t nseg = g.q > 0 ? g.n_level : g.r;
         const int gps = (int)((g.q + 1 + kChunk - 1) / kChunk);
-        hipLaunchKernelGGL((k_tree_extent<D>), dim3(nblocks(nseg * gps * 64)), dim3(kGbBlock), 0,
+        hipLaunchKernelGGL((k_tree_extent<D>), dim3(nblocks_capped(nseg * gps * 64)), dim3(kGbBlock), 0,
                            st, pa, g, nseg, gps, pmin, pmax, split);
         if (gps > 1)
             hipLaunchKernelGGL((k_tree_split<D>), dim3(nblocks(nseg)), dim3(kGbBlock), 0, st,
@@ -563,7 +580,7 @@ int build(const double* points, int64_t N, int64_t n0, int k, int lattice_bits, 
     hipLaunchKernelGGL((k_depth_gather<D>), dim3(nblocks(N)), dim3(kGbBlock), 0, st, N, val_b, pa,
                        perm_a, reinterpret_cast<const uint32_t*>(depth), pb, indices, key32a, inv);
     if (M > 0)
-        hipLaunchKernelGGL(k_nbr_remap, dim3(nblocks(M * k)), dim3(kGbBlock), 0, st, nbr, inv, n0,
+        hipLaunchKernelGGL(k_nbr_remap, dim3(nblocks_capped(M * k)), dim3(kGbBlock), 0, st, nbr, inv, n0,
                            M, k, neighbors);
 
     // 4. lattice: bounding box, step, rounding; level ends from the sorted depths
@@ -590,7 +607,7 @@ int build(const double* points, int64_t N, int64_t n0, int k, int lattice_bits, 
         extent = std::max(extent, hi - lo);
     }
     const double scale = extent > 0 ? extent / lmax : 1.0 / lmax;
-    hipLaunchKernelGGL((k_quantize<D>), dim3(nblocks(N * D)), dim3(kGbBlock), 0, st, pb, N, org,
+    hipLaunchKernelGGL((k_quantize<D>), dim3(nblocks_capped(N * D)), dim3(kGbBlock), 0, st, pb, N, org,
                        scale, lmax, coords);
     const int64_t n_off = (int64_t)last_depth + 1;
     if (n_off > offsets_cap)

@@ -43,7 +43,7 @@ struct Graph {
     std::vector<int64_t> offsets;  // host copy, offsets[0] = n0
     // Work lists of the one-launch sweeps: chunks of one level each, in topological order.
     // fwd: {first refined index m, points, 0, 0}; rev: {first position q, points | lg << 16,
-    // base, slots}, latest level first, the dense block last.
+    // base / kBlock, slots}, latest level first, the dense block last.
     int4* fwd_chunks = nullptr;
     int4* rev_chunks = nullptr;
     int n_fwd_chunks = 0, n_rev_chunks = 0;

@@ -145,8 +145,10 @@ int pack_graph(const uint32_t* coords, const int64_t* nbrs, const int64_t* offs,
                 if (((maxc + (1 << lg) - 1) >> lg) <= kPackRevSlots || lg == 6) break;
             }
             const int64_t nslots = (maxc + (1 << lg) - 1) >> lg;
+            // every chunk's entries start at a multiple of kPackBlock: the chunk stores its base
+            // in units of kPackBlock, which holds 2^31 * kPackBlock entries
             const int64_t base = (int64_t)rev.size();
-            if (base + nslots * kPackBlock >= ((int64_t)1 << 31))
+            if ((base >> kPackBaseShift) + nslots >= ((int64_t)1 << 31))
                 return pfail(err, GGP_ERR_ARG, "reverse neighbour lists too large");
             rev.resize((size_t)(base + nslots * kPackBlock), kPackRevNone);
             for (int64_t i = 0; i < np; ++i) {
@@ -156,7 +158,8 @@ int pack_graph(const uint32_t* coords, const int64_t* nbrs, const int64_t* offs,
                     rev[(size_t)(base + (u >> lg) * kPackBlock + lane)] = revl[(size_t)(rptr[(size_t)q] + u)];
                 }
             }
-            P.revc.push_back(Chunk{(int)s0, (int)(np | ((int64_t)lg << 16)), (int)base, (int)nslots});
+            P.revc.push_back(Chunk{(int)s0, (int)(np | ((int64_t)lg << 16)),
+                                   (int)(base >> kPackBaseShift), (int)nslots});
             s0 += np;
         }
     }

@@ -12,6 +12,8 @@ namespace ggp {
 constexpr int kPackBlock = 256;    // lanes per chunk of the one-launch sweeps (= kBlock)
 constexpr int kPackRevSlots = 16;  // reverse sweep: list entries per lane fetched together
 constexpr uint32_t kPackRevNone = 0xffffffffu;
+constexpr int kPackBaseShift = 8;  // reverse chunk bases are stored in units of 2^8 = kPackBlock
+static_assert((1 << kPackBaseShift) == kPackBlock, "chunk bases are multiples of the chunk width");
 
 // One work chunk of a sweep, in the layout of the device's int4.
 struct alignas(16) Chunk {
@@ -26,7 +28,8 @@ struct PackedGraph {
     std::vector<int32_t> nsoa;          // K*M: nbr[j*M + m], internal indices
     std::vector<uint32_t> rcnt;         // N: consumers of each internal position
     std::vector<uint32_t> rev;          // reverse lists, lane-major per reverse chunk
-    std::vector<Chunk> fwd, revc;       // sweep chunks in topological order
+    std::vector<Chunk> fwd, revc;       // sweep chunks in topological order (revc: {first
+                                        // position, points | lg << 16, base / kPackBlock, slots})
     std::vector<int32_t> idx32;         // N original positions (empty: identity)
     std::vector<uint32_t> coords;       // N*D, internal order
 };

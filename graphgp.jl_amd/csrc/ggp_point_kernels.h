@@ -301,10 +301,11 @@ k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
             for (int u = 0; u < B; ++u) {
                 const int t = t0 + u;
                 live[u] = pt && ((t << lg) + sub) < cnt;
-                // the chunk owns nslots * kBlock entries from ch.z (unused ones hold kRevNone),
+                // the chunk owns nslots * kBlock entries from ch.z * kBlock (unused ones hold
+                // kRevNone),
                 // so the entries are fetched with the counts, not after them; live implies
                 // t < nslots (a point's count is at most nslots << lg)
-                const uint32_t e = t < nslots ? rev[(int64_t)ch.z + (int64_t)t * kBlock + tid] : kRevNone;
+                const uint32_t e = t < nslots ? rev[((int64_t)ch.z + t) * kBlock + tid] : kRevNone;
                 const uint32_t m = e / KK, j = e - m * KK;
                 p[u] = n0 + m;
                 w[u] = live[u] ? mv[(int64_t)m * KK + j] : T(0);

@@ -70,7 +70,7 @@ static int check_pack(const std::vector<uint32_t>& coords, const std::vector<int
     int64_t prev_level = n_off + 1;
     for (const Chunk& c : P.revc) {
         const int lg = c.y >> 16, np = c.y & 0xffff;
-        const int64_t base = c.z, nslots = c.w;
+        const int64_t base = (int64_t)c.z << kPackBaseShift, nslots = c.w;
         if (np < 1 || np > (kPackBlock >> lg)) return bad("reverse chunk size");
         if (base < 0 || base + nslots * kPackBlock > (int64_t)P.rev.size()) return bad("reverse chunk range");
         const int64_t lv = level[(size_t)P.i2t[(size_t)c.x]];
