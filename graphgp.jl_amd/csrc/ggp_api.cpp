@@ -157,6 +157,43 @@ template <> struct Bits<double> {
     static double from(U u) { double x; std::memcpy(&x, &u, 8); return x; }
 };
 
+// O(1) segment index of a strictly increasing axis (nb >= 2) over the bit patterns of
+// [bins[1], bins[nb-1]] in at most umax cells: acc[c+1] is the largest lo <= nb-2 with bins[lo]
+// <= the smallest value of cell c (acc[0] = 0); steps is the most forward steps the search takes
+// from acc[cell] for any r < bins[nb-1] (the kernels use one unconditional step when <= 1).
+template <typename T>
+struct CellIndex {
+    std::vector<uint16_t> acc;
+    typename Bits<T>::U base = 0;
+    int shift = 0, ucells = 0, steps = 0;
+};
+template <typename T>
+CellIndex<T> cell_index(const T* bins, int64_t nb, int64_t umax) {
+    using U = typename Bits<T>::U;
+    CellIndex<T> ci;
+    ci.base = Bits<T>::of(bins[1]);
+    const U range = Bits<T>::of(bins[nb - 1]) - ci.base;
+    while ((int64_t)(range >> ci.shift) + 1 > umax) ++ci.shift;
+    ci.ucells = (int)((range >> ci.shift) + 1);
+    ci.acc.assign((size_t)ci.ucells + 1, 0);
+    int64_t lo = 1;
+    for (int c = 0; c < ci.ucells; ++c) {
+        const T cm = Bits<T>::from(ci.base + ((U)c << ci.shift));
+        while (lo + 1 <= nb - 2 && bins[lo + 1] <= cm) ++lo;
+        ci.acc[(size_t)c + 1] = (uint16_t)std::min<int64_t>(lo, nb - 2);
+    }
+    const U top_all = Bits<T>::of(bins[nb - 1]) - 1;
+    for (int c = 0; c < ci.ucells; ++c) {
+        const U top = std::min<U>(ci.base + (((U)c + 1) << ci.shift) - 1, top_all);
+        const T vmax = Bits<T>::from(top);
+        int64_t hi = ci.acc[(size_t)c + 1];
+        const int64_t lo0 = hi;
+        while (hi + 1 <= nb - 2 && bins[hi + 1] <= vmax) ++hi;
+        ci.steps = std::max<int>(ci.steps, (int)(hi - lo0));
+    }
+    return ci;
+}
+
 template <typename T>
 int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
     if (nb < 2) return fail(GGP_ERR_ARG, "nbins must be >= 2");
@@ -180,9 +217,6 @@ int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
         ent[i].slope = dy / dx;
     }
     // Cell index over bit patterns from bins[1] to bins[nb-1].
-    using U = typename Bits<T>::U;
-    const U base = Bits<T>::of(bins[1]);
-    const U range = Bits<T>::of(bins[nb - 1]) - base;
     const size_t entb = (size_t)(nb - 1) * sizeof(TabEnt<T>);
     // slack: the kernels' static LDS (reductions, the wavefront exchange slots)
     const size_t slack = 512 + (size_t)kWideBlock / 64 * 2 * 64 * sizeof(T);
@@ -194,38 +228,18 @@ int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
     // finer index there.
     const bool global = umax < kMinLdsCells;
     if (global) umax = std::min<int64_t>(65536, std::max<int64_t>(4096, 4 * nb));
-    int shift = 0;
-    while ((int64_t)(range >> shift) + 1 > umax) ++shift;
-    const int ucells = (int)((range >> shift) + 1);
-    std::vector<uint16_t> acc((size_t)ucells + 1);
-    acc[0] = 0;
-    int64_t lo = 1;
-    for (int c = 0; c < ucells; ++c) {
-        const T cm = Bits<T>::from(base + ((U)c << shift));
-        while (lo + 1 <= nb - 2 && bins[lo + 1] <= cm) ++lo;
-        acc[(size_t)c + 1] = (uint16_t)std::min<int64_t>(lo, nb - 2);
-    }
-    // Most forward steps the search takes from acc[cell] for any r < bins[nb-1] in the cell
-    // (the kernels use one unconditional step when this is <= 1).
-    int steps = 0;
-    const U top_all = Bits<T>::of(bins[nb - 1]) - 1;
-    for (int c = 0; c < ucells; ++c) {
-        const U top = std::min<U>(base + (((U)c + 1) << shift) - 1, top_all);
-        const T vmax = Bits<T>::from(top);
-        int64_t hi = acc[(size_t)c + 1];
-        const int64_t lo0 = hi;
-        while (hi + 1 <= nb - 2 && bins[hi + 1] <= vmax) ++hi;
-        steps = std::max<int>(steps, (int)(hi - lo0));
-    }
+    const CellIndex<T> ci = cell_index(bins, nb, umax);
+    const std::vector<uint16_t>& acc = ci.acc;
+    const int ucells = ci.ucells;
     TabParams<T> P{};
-    P.steps = steps;
+    P.steps = ci.steps;
     P.b0 = bins[0];
     P.b1 = bins[1];
     P.bl = bins[nb - 1];
     P.v0 = vals[0];
     P.vl = vals[nb - 1];
-    P.base = base;
-    P.shift = shift;
+    P.base = ci.base;
+    P.shift = ci.shift;
     P.ucells = ucells;
     P.nb = (int)nb;
     const bool realloc_tab = !tb.tab || tb.P.nb != (int)nb || tb.P.ucells != ucells;
@@ -309,17 +323,40 @@ int set_cov_aniso(ggp_graph* h, const T* sb, int64_t ns, const T* zb, int64_t nz
     host.insert(host.end(), grid, grid + ns * nz);
     for (const T& x : host)
         if (!std::isfinite(x)) return fail(GGP_ERR_ARG, "aniso table must be finite");
+    // O(1) cell indices of the two axes (the reference's _frac_index binary search,
+    // src/aniso.jl:43-57, finds the same segment); an axis of one entry never needs one
+    const CellIndex<T> si = ns >= 2 ? cell_index(sb, ns, std::max<int64_t>(64, 4 * ns)) : CellIndex<T>{};
+    const CellIndex<T> zi = nz >= 2 ? cell_index(zb, nz, std::max<int64_t>(64, 4 * nz)) : CellIndex<T>{};
+    std::vector<uint16_t> idx(si.acc);
+    if (idx.empty()) idx.push_back(0);
+    const size_t zoff = idx.size();
+    idx.insert(idx.end(), zi.acc.begin(), zi.acc.end());
+    if (idx.size() == zoff) idx.push_back(0);
+    const size_t tbytes = host.size() * sizeof(T);
     T* dev = nullptr;
     dfree(h, const_cast<T*>(tb.aniso.sb));  // the previous anisotropic table
     tb.aniso = AnisoArgs<T>{};
-    if (dmalloc(h, (void**)&dev, host.size() * sizeof(T))) return GGP_ERR_HIP;
-    HC(hipMemcpy(dev, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice));
+    if (dmalloc(h, (void**)&dev, tbytes + idx.size() * sizeof(uint16_t))) return GGP_ERR_HIP;
+    HC(hipMemcpy(dev, host.data(), tbytes, hipMemcpyHostToDevice));
+    uint16_t* didx = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(dev) + tbytes);
+    HC(hipMemcpy(didx, idx.data(), idx.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
     tb.aniso.sb = dev;
     tb.aniso.zb = dev + ns;
     tb.aniso.grid = dev + ns + nz;
+    tb.aniso.sacc = didx;
+    tb.aniso.zacc = didx + zoff;
+    tb.aniso.si.base = si.base;
+    tb.aniso.si.shift = si.shift;
+    tb.aniso.si.ucells = si.ucells;
+    tb.aniso.zi.base = zi.base;
+    tb.aniso.zi.shift = zi.shift;
+    tb.aniso.zi.ucells = zi.ucells;
     tb.aniso.ns = (int)ns;
     tb.aniso.nz = (int)nz;
     tb.aniso.alpha = (T)alpha;
+    // staged in LDS by the assembling kernels when the axes and indices fit the budget
+    const size_t sbytes = aniso_stage_bytes<T>((int)ns, (int)nz, si.ucells, zi.ucells);
+    tb.aniso.lds = sbytes + 1024 <= h->lds_max ? (int)sbytes : 0;
     tb.aniso_host = host;
     tb.global = false;
     // the isotropic table is not used by an anisotropic problem

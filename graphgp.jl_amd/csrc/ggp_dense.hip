@@ -32,20 +32,24 @@ __global__ void k_dense_assemble(T* __restrict__ A, const uint32_t* __restrict__
         for (int q = t; q < n_z0; q += 256) z0[q] = 0;
         for (int q = t; q < n_z1; q += 256) z1[q] = 0;
     }
+    if (blockIdx.x > blockIdx.y) return;  // the whole block lies above the diagonal
+    extern __shared__ __align__(16) unsigned char smem[];
+    AnisoArgs<T> av{};
+    if (ANISO) av = aniso_stage(an, smem);  // the whole workgroup, before any return
     const int j = blockIdx.x * 16 + threadIdx.x;
     const int i = blockIdx.y * 16 + threadIdx.y;
     if (i >= n || j > i) return;
     TabParams<T> P{};
     if (!ANISO) P = *Pp;
     if (i == j) {
-        const T d0 = ANISO ? aniso_lookup(T(0), T(0), an) : P.v0;
+        const T d0 = ANISO ? aniso_lookup(T(0), T(0), av) : P.v0;
         A[(int64_t)i * n + i] = diag_add == T(0) ? d0 : d0 + diag_add;
         return;
     }
     uint32_t ci[D], cj[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) { ci[d] = coords[(int64_t)i * D + d]; cj[d] = coords[(int64_t)j * D + d]; }
-    const T v = ANISO ? aniso_pair<T, D>(ci, cj, scale, an)
+    const T v = ANISO ? aniso_pair<T, D>(ci, cj, scale, av)
                       : cov_lookup(radius<T>(sqdist<D>(ci, cj), scale), tab, acc, P);
     A[(int64_t)i * n + j] = v;
     A[(int64_t)j * n + i] = v;
@@ -591,6 +595,162 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, in
     }
 }
 
+// ---- the same factor for large blocks: a few launches per tile column --------------------------
+// In the persistent launches above every 32 x 32 tile re-reads two input tiles per 32 terms, so
+// at a few thousand points the helpers' tile traffic and hand-offs, not arithmetic, set the
+// time. For large blocks the matrix is instead swept in super-panels of kSuper tile columns:
+//   k_panel_step (one launch per tile column s of the super-panel): workgroup i - s takes tile
+//     (i, s), adds the terms of the super-panel's earlier columns k in [32*s0, 32*s) from the
+//     finished tiles (i, k) and (s, k); workgroup 0 then factors the diagonal tile (the walker
+//     factor) and publishes it, and every other workgroup solves its tile against it (the walker
+//     solve). Workgroup 0 is dispatched first and waits for nothing, so the others' waits end.
+//   k_syrk_blk (one launch per super-panel): every kSyrkB x kSyrkB block of the trailing lower
+//     triangle receives the super-panel's kSuper*32 terms, k increasing, in register
+//     accumulators; the panel rows are staged in LDS a few columns at a time.
+// Entry (r, c) thus receives the terms of earlier super-panels through k_syrk_blk, then those of
+// its own super-panel through k_panel_step, every one in increasing k: the unblocked chain, so
+// the factor is bit-identical to the persistent launches' and to the oracle's.
+constexpr int kSuper = 4;     // tile columns per super-panel (128 terms per trailing update)
+constexpr int kSyrkB = 128;   // trailing-update block edge
+constexpr int kBlockedMin = 2049;  // blocks of at least this many points take this path
+
+template <typename T>
+__global__ void __launch_bounds__(kDfThreads) k_panel_step(T* __restrict__ A, int n, int s,
+                                                           int s0, int* __restrict__ flag,
+                                                           int* __restrict__ info) {
+    __shared__ T sA[kTile][kTile + 1];
+    __shared__ T sB[kTile][kTile + 1];
+    __shared__ T sC[kTile][kTile + 1];
+    __shared__ __align__(16) T sLt[kTile][kLtPitch];
+    __shared__ T sInv[kTile];
+    __shared__ __align__(16) T sCol[2][kTile];
+    const int tid = threadIdx.x;
+    const int c = tid & (kTile - 1), r0 = tid >> 5;
+    const int i = s + (int)blockIdx.x;
+    const int i0 = i * kTile, s0r = s * kTile;
+    T acc[4];
+    walk_load(acc, A, n, i, s, r0, c);
+    // the super-panel's finished columns (tiles k < s, all full: only the last tile column can
+    // be partial), rows past n read as zero
+    for (int k = s0; k < s; ++k) {
+        const int kk = k * kTile;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = r0 + 8 * q;
+            sA[r][c] = i0 + r < n ? A[(int64_t)(i0 + r) * n + kk + c] : T(0);
+            sB[r][c] = s0r + r < n ? A[(int64_t)(s0r + r) * n + kk + c] : T(0);
+        }
+        __syncthreads();
+        walk_term(acc, sA, sB, r0, c);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sA[r0 + 8 * q][c] = acc[q];
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        if (tid < 64) walk_factor_t(A, n, s, sA, sLt, sInv, (T*)nullptr, sCol, tid, info);
+        __syncthreads();
+        if (tid == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (tid == 0) df_wait(flag, info);
+    __syncthreads();
+    // L[s][s] transposed, zero above the diagonal (rows past n: the identity's)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = r0 + 8 * q;
+        T v = c <= r ? (s0r + r < n ? A[(int64_t)(s0r + r) * n + s0r + c] : T(r == c ? 1 : 0)) : T(0);
+        sLt[c][r] = v;
+    }
+    __syncthreads();
+    if (tid < 64) walk_solve_t(A, n, i, s, sA, sLt, sInv, sC, tid);
+}
+
+// A[r][c] = fma(-A[r][k], A[c][k], A[r][c]) for k = k0, ..., k0 + kd - 1 over the lower blocks of
+// the trailing matrix (r, c >= t0), one kSyrkB x kSyrkB block per workgroup: thread (ty, tx)
+// holds rows ty*8 .. ty*8+7 and columns tx*8 .. tx*8+7 of it. Diagonal blocks are computed
+// whole; their upper part lies in the unused upper triangle of A.
+template <typename T>
+__global__ void __launch_bounds__(256) k_syrk_blk(T* __restrict__ A, int n, int t0, int k0,
+                                                  int kd) {
+    constexpr int Kc = sizeof(T) == 4 ? 32 : 16;  // panel columns per LDS round
+    constexpr int P = kSyrkB + 4;                 // row pitch: 16-byte aligned rows
+    __shared__ __align__(16) T sa[Kc][P];         // sa[k][r] = A[R0 + r][k0 + kc + k]
+    __shared__ __align__(16) T sb[Kc][P];         // sb[k][c] = A[C0 + c][k0 + kc + k]
+    const int L = (int)blockIdx.x;
+    int I = (int)((__builtin_sqrt(8.0 * (double)L + 1.0) - 1.0) * 0.5);
+    while ((I + 1) * (I + 2) / 2 <= L) ++I;
+    while (I * (I + 1) / 2 > L) --I;
+    const int J = L - I * (I + 1) / 2;
+    const int R0 = t0 + I * kSyrkB, C0 = t0 + J * kSyrkB;
+    const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+    T acc[8][8];
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        const int r = R0 + ty * 8 + a;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const int cc = C0 + tx * 8 + b;
+            acc[a][b] = (r < n && cc < n) ? A[(int64_t)r * n + cc] : T(0);
+        }
+    }
+    for (int kc = 0; kc < kd; kc += Kc) {
+        __syncthreads();
+        // rows of the two panels, Kc consecutive columns each (k fastest: coalesced)
+        for (int e = tid; e < kSyrkB * Kc; e += 256) {
+            const int r = e / Kc, k = e - r * Kc;
+            const int64_t col = (int64_t)k0 + kc + k;
+            sa[k][r] = R0 + r < n ? A[(int64_t)(R0 + r) * n + col] : T(0);
+            sb[k][r] = C0 + r < n ? A[(int64_t)(C0 + r) * n + col] : T(0);
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int k = 0; k < Kc; ++k) {
+            T x[8], y[8];
+#pragma unroll
+            for (int a = 0; a < 8; ++a) x[a] = sa[k][ty * 8 + a];
+#pragma unroll
+            for (int b = 0; b < 8; ++b) y[b] = sb[k][tx * 8 + b];
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+#pragma unroll
+                for (int b = 0; b < 8; ++b) acc[a][b] = num<T>::fma(-x[a], y[b], acc[a][b]);
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        const int r = R0 + ty * 8 + a;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const int cc = C0 + tx * 8 + b;
+            if (r < n && cc < n) A[(int64_t)r * n + cc] = acc[a][b];
+        }
+    }
+}
+
+// Whether a block of n points takes the blocked path (GGP_POTRF_BLOCKED=1 / 0 forces it).
+bool dense_blocked(int n) {
+    if (const char* e = std::getenv("GGP_POTRF_BLOCKED")) return e[0] == '1';
+    return n >= kBlockedMin;
+}
+
+template <typename T>
+void dense_potrf_blocked(T* A, int n, int* info, int* flags, hipStream_t st) {
+    const int nt = (n + kTile - 1) / kTile;
+    for (int s0 = 0; s0 < nt; s0 += kSuper) {
+        const int s1 = std::min(nt, s0 + kSuper);
+        for (int s = s0; s < s1; ++s)
+            hipLaunchKernelGGL((k_panel_step<T>), dim3(nt - s), dim3(kDfThreads), 0, st, A, n, s,
+                               s0, flags + s, info);
+        const int t0 = s1 * kTile;
+        if (t0 < n) {
+            const int mb = (n - t0 + kSyrkB - 1) / kSyrkB;
+            hipLaunchKernelGGL((k_syrk_blk<T>), dim3(mb * (mb + 1) / 2), dim3(256), 0, st, A, n,
+                               t0, s0 * kTile, (s1 - s0) * kTile);
+        }
+    }
+}
+
 int dense_sync_ints(int n) {
     const int nt = (n + kTile - 1) / kTile;
     return dense_sync_flag_ints(nt) + 2 * nt * kTile;  // + the reciprocal diagonal (<= f64)
@@ -601,6 +761,10 @@ void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st, 
     if (n <= 0) return;
     const int nt = (n + kTile - 1) / kTile;
     if (!zeroed) launch_fill<int>(sync, 0, dense_sync_flag_ints(nt), st);
+    if (dense_blocked(n)) {
+        dense_potrf_blocked(A, n, info, sync + 1, st);  // flags: one per tile column
+        return;
+    }
     static const bool tiles = std::getenv("GGP_POTRF_TILES") != nullptr;
     if (tiles) {
         const int ntiles = nt * (nt + 1) / 2;
@@ -826,7 +990,7 @@ void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStr
     const bool an = tb.aniso.grid != nullptr;
 #define GGP_ASM(DD)                                                                             \
     do {                                                                                        \
-        if (an) hipLaunchKernelGGL((k_dense_assemble<T, DD, true>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso, zero_info, zero_info ? 1 : 0, zero_sync, nz1); \
+        if (an) hipLaunchKernelGGL((k_dense_assemble<T, DD, true>), grid, blk, tb.aniso.lds, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso, zero_info, zero_info ? 1 : 0, zero_sync, nz1); \
         else hipLaunchKernelGGL((k_dense_assemble<T, DD, false>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso, zero_info, zero_info ? 1 : 0, zero_sync, nz1); \
     } while (0)
     switch (g.D) {

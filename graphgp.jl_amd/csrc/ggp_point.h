@@ -248,34 +248,82 @@ __device__ inline bool pair_pts(const uint32_t (&ca)[D], const uint32_t (&cb)[D]
 }
 
 // ---- anisotropic covariance K(d_spatial, d_z) (src/aniso.jl) ----------------------------------
-// Device view of the table: axes sb (ns), zb (nz), grid[i*nz + j] = K(sb[i], zb[j]), alpha.
+// O(1) segment index of one axis of the grid: the cell index of TabParams over the IEEE bit
+// patterns of [bins[1], bins[n-1]]; acc[c+1] is the largest lo <= n-2 with bins[lo] <= the
+// smallest value of cell c.
+template <typename T> struct AxisIdx {
+    typename num<T>::bits_t base = 0;  // bits(bins[1])
+    int shift = 0, ucells = 0;
+};
+
+// Device view of the table: axes sb (ns), zb (nz), grid[i*nz + j] = K(sb[i], zb[j]), alpha, and
+// the axes' cell indices sacc (si.ucells + 1 entries) and zacc (zi.ucells + 1). The kernels that
+// assemble anisotropic covariances stage the axes and their indices in LDS (aniso_stage) when
+// `lds` bytes fit their budget; the grid is read from global memory (L2-resident).
 template <typename T> struct AnisoArgs {
     const T* sb = nullptr;
     const T* zb = nullptr;
     const T* grid = nullptr;
+    const uint16_t* sacc = nullptr;
+    const uint16_t* zacc = nullptr;
+    AxisIdx<T> si{}, zi{};
     int ns = 0, nz = 0;
     T alpha = T(1);
+    int lds = 0;  // bytes of the staged axes and indices, 0: not staged
 };
 
 // _frac_index (src/aniso.jl:43-57): 0-based fractional position of d on an increasing axis,
-// clamped to [0, n-1]; the bracketing segment is the binary search's (Julia tie rule).
+// clamped to [0, n-1]. The bracketing segment is the binary search's (Julia tie rule: the
+// largest lo with bins[lo] <= d), found from the cell index and forward steps.
 template <typename T>
-__device__ inline T frac_index(T d, const T* __restrict__ bins, int n) {
+__device__ inline T frac_index(T d, const T* __restrict__ bins, int n,
+                               const uint16_t* __restrict__ acc, const AxisIdx<T>& X) {
     if (d <= bins[0]) return T(0);
     if (d >= bins[n - 1]) return T(n - 1);
-    int lo = 0, hi = n - 1;
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (bins[mid] <= d) lo = mid; else hi = mid;
-    }
+    using S = typename num<T>::sbits_t;
+    const S dd = (S)(num<T>::bits(d) - X.base);
+    const int cell = dd < 0 ? 0 : (int)min((S)(dd >> X.shift) + 1, (S)X.ucells);
+    int lo = acc[cell];
+    while (bins[lo + 1] <= d) ++lo;  // bounded: d < bins[n-1]
     const T x0 = bins[lo], x1 = bins[lo + 1];
     return T(lo) + (d - x0) / (x1 - x0);
+}
+
+// The axes and their cell indices copied into LDS at smem (an.lds bytes) by the whole
+// workgroup; returns the view to use (an itself when the axes are not staged).
+template <typename T>
+__device__ inline AnisoArgs<T> aniso_stage(const AnisoArgs<T>& an, unsigned char* smem) {
+    if (an.lds == 0) return an;
+    AnisoArgs<T> s = an;
+    T* sb = reinterpret_cast<T*>(smem);
+    T* zb = sb + an.ns;
+    uint16_t* sacc = reinterpret_cast<uint16_t*>(zb + an.nz);
+    uint16_t* zacc = sacc + an.si.ucells + 1;
+    const int t = (int)(threadIdx.x + blockDim.x * (threadIdx.y + blockDim.y * threadIdx.z));
+    const int nth = (int)(blockDim.x * blockDim.y * blockDim.z);
+    for (int i = t; i < an.ns; i += nth) sb[i] = an.sb[i];
+    for (int i = t; i < an.nz; i += nth) zb[i] = an.zb[i];
+    for (int i = t; i <= an.si.ucells; i += nth) sacc[i] = an.sacc[i];
+    for (int i = t; i <= an.zi.ucells; i += nth) zacc[i] = an.zacc[i];
+    __syncthreads();
+    s.sb = sb;
+    s.zb = zb;
+    s.sacc = sacc;
+    s.zacc = zacc;
+    return s;
+}
+
+// Bytes aniso_stage needs: both axes, then both cell indices.
+template <typename T>
+__host__ __device__ inline size_t aniso_stage_bytes(int ns, int nz, int su, int zu) {
+    return (size_t)(ns + nz) * sizeof(T) + (size_t)(su + 1 + zu + 1) * sizeof(uint16_t);
 }
 
 // aniso_lookup (src/aniso.jl:66-84): bilinear interpolation with edge clamping; no @fastmath.
 template <typename T>
 __device__ inline T aniso_lookup(T ds, T dz, const AnisoArgs<T>& a) {
-    const T fx = frac_index(ds, a.sb, a.ns), fz = frac_index(dz, a.zb, a.nz);
+    const T fx = frac_index(ds, a.sb, a.ns, a.sacc, a.si);
+    const T fz = frac_index(dz, a.zb, a.nz, a.zacc, a.zi);
     const int i0 = (int)fx, j0 = (int)fz;
     const int i1 = i0 + 1 < a.ns ? i0 + 1 : a.ns - 1, j1 = j0 + 1 < a.nz ? j0 + 1 : a.nz - 1;
     const T tx = fx - T(i0), tz = fz - T(j0);

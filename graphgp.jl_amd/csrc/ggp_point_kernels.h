@@ -117,15 +117,18 @@ k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, i
         stage_table(s_tab, s_acc, g_tab, g_acc, P);
     }
 
+    AnisoArgs<T> av{};
+    if (ANISO) av = aniso_stage(an, smem);
+
     double lsum = 0.0;
     if (ANISO || P.steps <= 1)
         lsum = factor_points<T, K, D, MODE, ANISO, true>(coords, nbr, M, n0, scale, s_tab, s_acc,
-                                                         P, mv, sd, terms, values, xi_out, an,
-                                                         nbr64);
+                                                         P, mv, sd, terms, values,
+                                                         xi_out, av, nbr64);
     else
         lsum = factor_points<T, K, D, MODE, ANISO, false>(coords, nbr, M, n0, scale, s_tab, s_acc,
-                                                          P, mv, sd, terms, values, xi_out, an,
-                                                          nbr64);
+                                                          P, mv, sd, terms, values,
+                                                          xi_out, av, nbr64);
     if (MODE & F_TERMS) {
         const double t = block_sum(lsum, s_red);
         if (threadIdx.x == 0) partial[blockIdx.x] = t;
@@ -302,9 +305,8 @@ k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
                 const int t = t0 + u;
                 live[u] = pt && ((t << lg) + sub) < cnt;
                 // the chunk owns nslots * kBlock entries from ch.z * kBlock (unused ones hold
-                // kRevNone),
-                // so the entries are fetched with the counts, not after them; live implies
-                // t < nslots (a point's count is at most nslots << lg)
+                // kRevNone), so the entries are fetched with the counts, not after them; live
+                // implies t < nslots (a point's count is at most nslots << lg)
                 const uint32_t e = t < nslots ? rev[((int64_t)ch.z + t) * kBlock + tid] : kRevNone;
                 const uint32_t m = e / KK, j = e - m * KK;
                 p[u] = n0 + m;
@@ -529,12 +531,12 @@ void PointK<T, K>::factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T
                           double* partial, const T* values, T* xi_out, unsigned nblk,
                           hipStream_t st) {
     const bool aniso = tb.aniso.grid != nullptr;
-    const size_t lds = aniso ? 0 : tab_bytes<T>(tb.P.nb, tb.P.ucells);
+    const size_t lds = aniso ? (size_t)tb.aniso.lds : tab_bytes<T>(tb.P.nb, tb.P.ucells);
     const T scale = (T)g.scale;
 #define GGP_FACTOR(DD, MODEV)                                                                  \
     do {                                                                                       \
         if (aniso)                                                                             \
-            hipLaunchKernelGGL((k_factor<T, K, DD, MODEV, true>), dim3(nblk), dim3(kBlock), 0,  \
+            hipLaunchKernelGGL((k_factor<T, K, DD, MODEV, true>), dim3(nblk), dim3(kBlock), lds,\
                                st, g.coords, g.nbr, g.M, g.n0, scale, tb.tab, tb.acc,           \
                                tb.params, mv, sd, terms, partial, values, xi_out, tb.aniso,     \
                                g.nbr64);                                                        \

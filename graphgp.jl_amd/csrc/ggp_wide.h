@@ -171,6 +171,8 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
             stage_table(s_tab, s_acc, g_tab, g_acc, P);
         }
     }
+    AnisoArgs<T> av{};
+    if (ANISO) av = aniso_stage(an, smem);
     const int lane = threadIdx.x & 63;
     const int n = K + 1;
     double lsum = 0.0;
@@ -179,7 +181,7 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
         uint32_t x[D];
         const int32_t nb = wide_gather<D>(x, coords, nbr, M, m, n0, K, lane, nbr64);
         T a[kWideN], unused[kWideN];
-        wide_assemble<T, D, ANISO>(a, x, n, lane, scale, s_tab, s_acc, P, an);
+        wide_assemble<T, D, ANISO>(a, x, n, lane, scale, s_tab, s_acc, P, av);
         const T s = wide_cholesky<T, false>(a, unused, n, K, lane);
         if (mode & F_TERMS) {
             const T t = num<T>::log(s);

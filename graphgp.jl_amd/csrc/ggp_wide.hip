@@ -21,7 +21,8 @@ void WideD<T, D>::factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T*
                       double* partial, const T* values, T* xi_out, unsigned nblk,
                       hipStream_t st) {
     const bool aniso = tb.aniso.grid != nullptr;
-    const size_t lds = aniso || tb.global ? 0 : tab_bytes<T>(tb.P.nb, tb.P.ucells);
+    const size_t lds = aniso ? (size_t)tb.aniso.lds
+                             : tb.global ? 0 : tab_bytes<T>(tb.P.nb, tb.P.ucells);
     const T scale = (T)g.scale;
     const int K = (int)g.K;
     // TERMS writes one partial per launched workgroup: keep the grid at nblk so the host's
@@ -37,7 +38,7 @@ void WideD<T, D>::factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T*
     do {                                                                                       \
         if (aniso)                                                                             \
             hipLaunchKernelGGL((k_factor_w<T, D, MODEV, true, false>), dim3(grid),              \
-                               dim3(kWideBlock), 0, st, g.coords, g.nbr, g.M, g.n0, K, scale,   \
+                               dim3(kWideBlock), lds, st, g.coords, g.nbr, g.M, g.n0, K, scale, \
                                tb.tab, tb.acc, tb.params, mv, sd, terms, partial, values,       \
                                xi_out, tb.aniso, g.nbr64, 0);                                   \
         else                                                                                   \

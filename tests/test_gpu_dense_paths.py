@@ -1,0 +1,86 @@
+"""The two schedules of the dense first-layer Cholesky (the persistent walker launch and the
+blocked path of panel steps plus trailing updates, which large blocks take) against the oracle's
+column-by-column factor.
+
+Both schedules give every entry of the factor the unblocked left-looking fma chain in the same
+order, so the dense part of generate (L xi, a product whose chain is also the oracle's) must
+have the oracle's bits in Float32 and Float64, whichever schedule ran. GGP_POTRF_BLOCKED forces
+the schedule (read at every call).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import relerr
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def G():
+    import graphgp_hip
+    return graphgp_hip
+
+
+def O():
+    import oracle
+    return oracle
+
+
+def _problem(N, n0, dtype, seed):
+    rng = np.random.default_rng(seed)
+    pts = rng.random((N, 3))
+    bins, vals = G().rbf_kernel(1.0, 0.2, 1e-4, 2.0, 400, jitter=1e-4)
+    prob = G().build_graph(pts, n0, 8, bins.astype(dtype), vals.astype(dtype))
+    ref = O().Problem(prob.coords, prob.neighbors, prob.offsets, prob.n0, prob.scale, prob.bins,
+                      prob.vals, indices=prob.indices, dtype=dtype)
+    return prob, ref, rng
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("n0", [300, 1000, 1500])
+def test_blocked_and_walker_factor_bit_exact(gpu, monkeypatch, n0, dtype):
+    _say(f"case dense schedules n0={n0} {np.dtype(dtype).name}")
+    prob, ref, rng = _problem(n0 + 500, n0, dtype, seed=n0)
+    hp = G().to_backend(prob)
+    xi = rng.standard_normal(prob.N).astype(dtype)
+    want = ref.generate(xi)
+    ld_want = ref.generate_logdet()
+    out = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("GGP_POTRF_BLOCKED", mode)
+        f = G().generate(hp, xi)
+        ld = G().generate_logdet(hp)
+        _say(f"  blocked={mode}: generate relerr {relerr(f, want):.3e}, "
+             f"logdet {abs(ld - ld_want) / abs(ld_want):.3e}")
+        np.testing.assert_array_equal(f, want)
+        assert abs(ld - ld_want) <= (1e-12 if dtype == np.float64 else 1e-5) * abs(ld_want)
+        out[mode] = f
+    np.testing.assert_array_equal(out["0"], out["1"])
+
+
+def test_blocked_factor_not_positive_definite_retry(gpu, monkeypatch):
+    """A covariance without jitter on coincident points fails the first factorization; the
+    blocked schedule reports the pivot like the walker, and the jitter retry succeeds."""
+    _say("case dense blocked retry")
+    rng = np.random.default_rng(5)
+    bins, vals = G().rbf_kernel(1.0, 0.2, 1e-4, 2.0, 400, jitter=0.0)
+    base = G().build_graph(rng.random((900, 3)), 600, 8, bins, vals)
+    coords = base.coords.copy()
+    coords[5] = coords[3]
+    coords[407] = coords[3]
+    prob = G().GraphGPProblem(coords, base.neighbors, base.offsets, base.n0, base.scale,
+                              base.bins, base.vals, indices=base.indices)
+    hp = G().to_backend(prob)
+    xi = rng.standard_normal(prob.N)
+    res = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("GGP_POTRF_BLOCKED", mode)
+        res[mode] = G().generate(hp, xi)
+        assert np.all(np.isfinite(res[mode]))
+    np.testing.assert_array_equal(res["0"], res["1"])
