@@ -584,12 +584,12 @@ int op_generate_inv(ggp_graph* h, const T* values, T* xi_out, hipStream_t user) 
     launch_gather<T>(vt, values, g.idx, g.N, h->s_main);
     factor_t<T>(h, F_INV, nullptr, nullptr, nullptr, nullptr, vt, xt + g.n0);
     if (int rc = join(h)) return rc;
-    dense_trsv<T>(tp<T>(h->A), (int)g.n0, vt, xt, h->s_main);
+    dense_trsv<T>(tp<T>(h->A), (int)g.n0, vt, xt, h->dsync, h->info, h->s_main);
     launch_scatter<T>(xi_out, xt, g.idx, g.N, h->s_main);
     if (int rc = finish(h, user)) return rc;
     if (*h->hinfo != 0) {
         if (int rc = dense_retry<T>(h)) return rc;
-        dense_trsv<T>(tp<T>(h->A), (int)g.n0, vt, xt, h->s_main);
+        dense_trsv<T>(tp<T>(h->A), (int)g.n0, vt, xt, h->dsync, h->info, h->s_main);
         launch_scatter<T>(xi_out, xt, g.idx, g.N, h->s_main);
         HC(hipStreamSynchronize(h->s_main));
     }
@@ -727,8 +727,8 @@ void dense_grad(ggp_graph* h, int kind, hipStream_t st, bool inverse_ready = fal
         // xi_dense = L \ y, alpha = L^-T xi_dense (src/dense.jl:229-240).
         T* xid = tp<T>(h->xt);
         T* alpha = tp<T>(h->tmp);
-        dense_trsv<T>(tp<T>(h->A), n, tp<T>(h->v), xid, st);
-        dense_trsv_t<T>(tp<T>(h->A), n, xid, alpha, st);
+        dense_trsv<T>(tp<T>(h->A), n, tp<T>(h->v), xid, h->dsync, h->info, st);
+        dense_trsv_t<T>(tp<T>(h->A), n, xid, alpha, h->dsync, h->info, st);
         launch_sumsq_half<T>(xid, n, h->dscal + 1, st);
         dense_grad_invloss<T>(g, tb, alpha, rows, h->nw_dense, st);
     }
@@ -868,8 +868,8 @@ int op_grad_points(ggp_graph* h, int mode, bool dense, const T* in, T* d_points,
             // xi_dense = L \ y, alpha = L^-T xi_dense (src/dense.jl:271-300)
             T* xid = tp<T>(h->xt);
             T* alpha = tp<T>(h->tmp);
-            dense_trsv<T>(tp<T>(h->A), n, v, xid, st);
-            dense_trsv_t<T>(tp<T>(h->A), n, xid, alpha, st);
+            dense_trsv<T>(tp<T>(h->A), n, v, xid, h->dsync, h->info, st);
+            dense_trsv_t<T>(tp<T>(h->A), n, xid, alpha, h->dsync, h->info, st);
             launch_sumsq_half<T>(xid, n, h->dscal + 1, st);
             dense_grad_points_invloss<T>(g, tb, alpha, h->dpd, st);
         }

@@ -89,6 +89,21 @@ __device__ inline void df_wait(const int* flag, int* info) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
+// df_wait for a whole wavefront in uniform control flow: every lane polls the same flag, and the
+// value is made wave-uniform so the loop's exit is too.
+__device__ inline void df_wait_uniform(const int* flag, int* info) {
+    int spins = 0;
+    while (__builtin_amdgcn_readfirstlane(
+               __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > kDfSpinLimit) {
+            atomicOr(info, 2);
+            break;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
 // sync = [ticket, flags[nt * nt]] (zeroed before the launch).
 template <typename T>
 __global__ void __launch_bounds__(kDfThreads) k_potrf_tiles(T* __restrict__ A, int n, int nt,
@@ -880,64 +895,66 @@ __global__ void __launch_bounds__(256) k_trmv_t(const T* __restrict__ L, int n,
     }
 }
 
-// x = L \ b (src/dense.jl:134), one workgroup: 32-row diagonal blocks solved by wave 0 with
-// broadcasts, the rows below updated by all threads; per entry the same fma chain as the
-// row-by-row substitution.
-template <typename T>
-__global__ void __launch_bounds__(256) k_trsv(const T* __restrict__ L, int n,
-                                              const T* __restrict__ b, T* __restrict__ x) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = b[i];
-    __syncthreads();
-    for (int k0 = 0; k0 < n; k0 += kTile) {
-        const int nk = min(kTile, n - k0);
-        if (threadIdx.x < 64) {
-            const int lane = threadIdx.x;
-            T v = lane < nk ? x[k0 + lane] : T(0);
-            for (int jj = 0; jj < nk; ++jj) {
-                const T xj = bcast(v, jj) / L[(int64_t)(k0 + jj) * n + k0 + jj];
-                if (lane == jj) v = xj;
-                else if (lane > jj && lane < nk)
-                    v = num<T>::fma(-L[(int64_t)(k0 + lane) * n + k0 + jj], xj, v);
+// x = L \ b (src/dense.jl:134) and x = L^T \ b (src/dense.jl:236): the row-by-row
+// substitutions, each row's fma chain in the serial order (the earlier unknowns in increasing
+// index for L, decreasing blocks of 32 for L^T), then its division. One wavefront per 32-row
+// block; blocks are taken from a ticket counter in the order of the substitution (forward
+// for L, backward for L^T), so a block waits only for blocks taken earlier by running
+// wavefronts and the launch cannot deadlock. A block folds in each earlier block's unknowns as
+// soon as they are published (release / acquire of a per-block flag), so only the last block's
+// terms and the block's own 32-step solve stay on the chain from block to block. Every wait is
+// bounded (bit 1 of *info when exceeded). sync = [ticket, flags[nt]], zeroed by the caller.
+template <typename T, bool TRANS>
+__global__ void __launch_bounds__(64) k_trsv_mw(const T* __restrict__ L, int n, int nt,
+                                                const T* __restrict__ b, T* __restrict__ x,
+                                                int* __restrict__ sync, int* __restrict__ info) {
+    int* ticket = sync;
+    int* flags = sync + 1;
+    const int lane = threadIdx.x;
+    // Every lane runs the ticket, wait and publish steps (uniform control flow: with a
+    // lane-0-only branch around them the compiler may let the other lanes run ahead into the
+    // next block on a stale ticket). Only lane 0 adds to the ticket; every lane polls the flag
+    // (one request per wavefront) and stores the same flag value.
+    while (true) {
+        const int t = __builtin_amdgcn_readfirstlane(atomicAdd(ticket, lane == 0 ? 1 : 0));
+        if (t >= nt) break;
+        const int blk = TRANS ? nt - 1 - t : t;
+        const int i0 = blk * kTile, ni = min(kTile, n - i0);
+        const bool live = lane < ni;
+        T v = live ? b[i0 + lane] : T(0);
+        for (int q = 0; q < t; ++q) {
+            const int kb = TRANS ? nt - 1 - q : q;
+            const int k0 = kb * kTile, nk = min(kTile, n - k0);
+            df_wait_uniform(&flags[kb], info);
+            T xk[kTile], lr[kTile];
+#pragma unroll
+            for (int p = 0; p < kTile; ++p) {
+                xk[p] = p < nk ? x[k0 + p] : T(0);
+                lr[p] = (live && p < nk) ? (TRANS ? L[(int64_t)(k0 + p) * n + i0 + lane]
+                                                  : L[(int64_t)(i0 + lane) * n + k0 + p])
+                                         : T(0);
             }
-            if (lane < nk) x[k0 + lane] = v;
+#pragma unroll
+            for (int p = 0; p < kTile; ++p)
+                if (p < nk) v = num<T>::fma(-lr[p], xk[p], v);
         }
-        __syncthreads();
-        for (int i = k0 + nk + threadIdx.x; i < n; i += blockDim.x) {
-            T s = x[i];
-            const T* row = L + (int64_t)i * n + k0;
-            for (int p = 0; p < nk; ++p) s = num<T>::fma(-row[p], x[k0 + p], s);
-            x[i] = s;
-        }
-        __syncthreads();
-    }
-}
-
-// x = L^T \ b (src/dense.jl:236), blocked backward substitution.
-template <typename T>
-__global__ void __launch_bounds__(256) k_trsv_t(const T* __restrict__ L, int n,
-                                                const T* __restrict__ b, T* __restrict__ x) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = b[i];
-    __syncthreads();
-    const int nt = (n + kTile - 1) / kTile;
-    for (int kb = nt - 1; kb >= 0; --kb) {
-        const int k0 = kb * kTile, nk = min(kTile, n - k0);
-        if (threadIdx.x < 64) {
-            const int lane = threadIdx.x;
-            T v = lane < nk ? x[k0 + lane] : T(0);
-            for (int jj = nk - 1; jj >= 0; --jj) {
-                const T xj = bcast(v, jj) / L[(int64_t)(k0 + jj) * n + k0 + jj];
+        // the block's own unknowns, by broadcasts (same chains as the serial substitution)
+        if (!TRANS) {
+            for (int jj = 0; jj < ni; ++jj) {
+                const T xj = bcast(v, jj) / L[(int64_t)(i0 + jj) * n + i0 + jj];
                 if (lane == jj) v = xj;
-                else if (lane < jj) v = num<T>::fma(-L[(int64_t)(k0 + jj) * n + k0 + lane], xj, v);
+                else if (lane > jj && lane < ni)
+                    v = num<T>::fma(-L[(int64_t)(i0 + lane) * n + i0 + jj], xj, v);
             }
-            if (lane < nk) x[k0 + lane] = v;
+        } else {
+            for (int jj = ni - 1; jj >= 0; --jj) {
+                const T xj = bcast(v, jj) / L[(int64_t)(i0 + jj) * n + i0 + jj];
+                if (lane == jj) v = xj;
+                else if (lane < jj) v = num<T>::fma(-L[(int64_t)(i0 + jj) * n + i0 + lane], xj, v);
+            }
         }
-        __syncthreads();
-        for (int i = threadIdx.x; i < k0; i += blockDim.x) {
-            T s = x[i];
-            for (int p = 0; p < nk; ++p) s = num<T>::fma(-L[(int64_t)(k0 + p) * n + i], x[k0 + p], s);
-            x[i] = s;
-        }
-        __syncthreads();
+        if (live) x[i0 + lane] = v;
+        __hip_atomic_store(&flags[blk], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -967,13 +984,21 @@ void dense_trmv_t(const T* L, int n, const T* x, T* y, hipStream_t st, T* out,
     hipLaunchKernelGGL((k_trmv_t<T, T, T>), dim3(cdiv(n, kTvRows)), dim3(256), 0, st, L, n, x, y,
                        out, oidx);
 }
-template <typename T>
-void dense_trsv(const T* L, int n, const T* b, T* x, hipStream_t st) {
-    hipLaunchKernelGGL((k_trsv<T>), dim3(1), dim3(256), 0, st, L, n, b, x);
+template <typename T, bool TRANS>
+static void trsv_mw(const T* L, int n, const T* b, T* x, int* sync, int* info, hipStream_t st) {
+    if (n <= 0) return;
+    const int nt = (n + kTile - 1) / kTile;
+    launch_fill<int>(sync, 0, nt + 1, st);
+    hipLaunchKernelGGL((k_trsv_mw<T, TRANS>), dim3(std::min(nt, 1024)), dim3(64), 0, st, L, n, nt,
+                       b, x, sync, info);
 }
 template <typename T>
-void dense_trsv_t(const T* L, int n, const T* b, T* x, hipStream_t st) {
-    hipLaunchKernelGGL((k_trsv_t<T>), dim3(1), dim3(256), 0, st, L, n, b, x);
+void dense_trsv(const T* L, int n, const T* b, T* x, int* sync, int* info, hipStream_t st) {
+    trsv_mw<T, false>(L, n, b, x, sync, info, st);
+}
+template <typename T>
+void dense_trsv_t(const T* L, int n, const T* b, T* x, int* sync, int* info, hipStream_t st) {
+    trsv_mw<T, true>(L, n, b, x, sync, info, st);
 }
 template <typename T>
 void dense_logdiag(const T* L, int n, double* out, hipStream_t st) {
@@ -1468,8 +1493,8 @@ void dense_grad_points_invloss(const Graph& g, const Table<T>& tb, const T* alph
     template void dense_trmv<T>(const T*, int, const T*, T*, hipStream_t, T*, const int32_t*); \
     template void dense_trmv_t<T>(const T*, int, const T*, T*, hipStream_t, T*,                \
                                   const int32_t*);                                             \
-    template void dense_trsv<T>(const T*, int, const T*, T*, hipStream_t);                     \
-    template void dense_trsv_t<T>(const T*, int, const T*, T*, hipStream_t);                   \
+    template void dense_trsv<T>(const T*, int, const T*, T*, int*, int*, hipStream_t);         \
+    template void dense_trsv_t<T>(const T*, int, const T*, T*, int*, int*, hipStream_t);       \
     template void dense_logdiag<T>(const T*, int, double*, hipStream_t);                       \
     template void dense_grad_logdet<T>(const Graph&, const Table<T>&, const T*, double*,       \
                                        double*, double*, int, hipStream_t);                    \

@@ -224,10 +224,12 @@ void dense_trmv(const T* L, int n, const T* x, T* y, hipStream_t st, T* out = nu
 template <typename T>
 void dense_trmv_t(const T* L, int n, const T* x, T* y, hipStream_t st, T* out = nullptr,
                   const int32_t* oidx = nullptr);
+// Triangular solves x = L \ b and x = L^T \ b. sync: nt + 1 ints of scratch (nt = ceil(n/32)),
+// zeroed by the solve itself; *info bit 1 reports a wait past its bound.
 template <typename T>
-void dense_trsv(const T* L, int n, const T* b, T* x, hipStream_t st);
+void dense_trsv(const T* L, int n, const T* b, T* x, int* sync, int* info, hipStream_t st);
 template <typename T>
-void dense_trsv_t(const T* L, int n, const T* b, T* x, hipStream_t st);
+void dense_trsv_t(const T* L, int n, const T* b, T* x, int* sync, int* info, hipStream_t st);
 template <typename T>
 void dense_logdiag(const T* L, int n, double* out, hipStream_t st);
 // Dense cotangent pipelines (f64 internally). Each writes d/dvals of the dense term, accumulated
