@@ -218,8 +218,7 @@ int set_cov(ggp_graph* h, const T* bins, const T* vals, int64_t nb) {
     }
     // Cell index over bit patterns from bins[1] to bins[nb-1].
     const size_t entb = (size_t)(nb - 1) * sizeof(TabEnt<T>);
-    // slack: the kernels' static LDS (reductions, the wavefront exchange slots)
-    const size_t slack = 512 + (size_t)kWideBlock / 64 * 2 * 64 * sizeof(T);
+    const size_t slack = lds_slack<T>(h->g.K);
     size_t budget = h->lds_max > entb + (size_t)nb * 8 + slack ? h->lds_max - entb - (size_t)nb * 8 - slack : 0;
     int64_t umax = std::min<int64_t>(4096, (int64_t)(budget / 2) - 1);
     // Too little LDS left for a useful cell index: the table stays in global memory (the
@@ -356,7 +355,7 @@ int set_cov_aniso(ggp_graph* h, const T* sb, int64_t ns, const T* zb, int64_t nz
     tb.aniso.alpha = (T)alpha;
     // staged in LDS by the assembling kernels when the axes and indices fit the budget
     const size_t sbytes = aniso_stage_bytes<T>((int)ns, (int)nz, si.ucells, zi.ucells);
-    tb.aniso.lds = sbytes + 1024 <= h->lds_max ? (int)sbytes : 0;
+    tb.aniso.lds = sbytes + lds_slack<T>(h->g.K) <= h->lds_max ? (int)sbytes : 0;
     tb.aniso_host = host;
     tb.global = false;
     // the isotropic table is not used by an anisotropic problem
@@ -931,8 +930,8 @@ int create(ggp_graph** out, const uint32_t* coords, const int64_t* nbrs, const i
     else h->nblk_factor = (unsigned)(h->ncu * 4);
     if (const char* e = std::getenv("GGP_PULL_BLOCKS_PER_CU")) h->nblk_pull = (unsigned)(h->ncu * std::max(1, atoi(e)));
     else h->nblk_pull = (unsigned)(h->ncu * 6);  // the table + histogram LDS admits ~5 per CU
-    // points per workgroup pass: kBlock (a lane per point) or kWideBlock/64 (a wavefront per point)
-    const int64_t ppb = register_block_k(k) ? kBlock : kWideBlock / 64;
+    // points per workgroup pass: kBlock (a lane per point) or kWidePts (32 lanes per point)
+    const int64_t ppb = register_block_k(k) ? kBlock : kWidePts;
     if (!register_block_k(k)) {
         if (!std::getenv("GGP_FACTOR_BLOCKS_PER_CU")) h->nblk_factor = (unsigned)(h->ncu * 8);
         if (!std::getenv("GGP_PULL_BLOCKS_PER_CU")) h->nblk_pull = (unsigned)(h->ncu * 4);

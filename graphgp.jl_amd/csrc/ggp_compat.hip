@@ -45,9 +45,9 @@ struct CompatLayout {
 // beside the table (and a histogram), or, when that is too little, a table in global memory
 // (*global set) with a finer index there.
 template <typename T>
-int cells_for(int64_t nb, size_t lds_max, bool* global) {
+int cells_for(int64_t nb, int64_t k, size_t lds_max, bool* global) {
     const size_t entb = (size_t)(nb - 1) * sizeof(TabEnt<T>);
-    const size_t slack = 512 + (size_t)kWideBlock / 64 * 2 * 64 * sizeof(T);
+    const size_t slack = lds_slack<T>(k);
     const size_t hist = (size_t)nb * 8;
     const size_t budget = lds_max > entb + hist + slack ? lds_max - entb - hist - slack : 0;
     const int64_t cells = std::min<int64_t>(kCompatMaxCells, (int64_t)(budget / 2) - 1);
@@ -202,7 +202,7 @@ int check(const CompatArgs& a, int op) {
 // Workgroups of the factor launch: the handle path's grid for this k, at most kCompatMaxBlocks.
 unsigned factor_blocks(int64_t M, int64_t k, int ncu) {
     const bool reg = register_block_k(k);
-    const int64_t ppb = reg ? kBlock : kWideBlock / 64;
+    const int64_t ppb = reg ? kBlock : kWidePts;
     const int64_t want = reg ? (int64_t)ncu * 4 : (int64_t)ncu * 8;
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>({want, (M + ppb - 1) / ppb,
                                                               (int64_t)kCompatMaxBlocks}));
@@ -212,7 +212,7 @@ unsigned factor_blocks(int64_t M, int64_t k, int ncu) {
 template <typename T>
 size_t scratch_bytes(const CompatArgs& a, const DevInfo& d, int* cells_out, unsigned* nblk_out,
                      bool* global) {
-    const int cells = cells_for<T>(a.nb, d.lds, global);
+    const int cells = cells_for<T>(a.nb, a.k, d.lds, global);
     const unsigned nblk = factor_blocks(a.N - a.n0, a.k, d.ncu);
     *cells_out = cells;
     *nblk_out = nblk;

@@ -12,7 +12,15 @@ namespace ggp {
 
 constexpr int kBlock = 256;    // threads per workgroup of the per-point kernels
 constexpr int kTile = 32;      // dense-layer tile edge
-constexpr int kWideBlock = 256;  // threads per workgroup of the wavefront-per-point kernels
+constexpr int kWideBlock = 256;  // threads per workgroup of the group-per-point kernels (k <= 31)
+constexpr int kWidePts = kWideBlock / 32;  // points per workgroup pass there (32 lanes each)
+constexpr int kWideXch = 144;    // exchange area per point there, in elements of T
+// Static LDS of one workgroup of those kernels: per point its rows' coordinates (32 x 4 words),
+// a seed vector (32 T) and the exchange area; plus the block reduction.
+template <typename T>
+constexpr size_t wide_static_lds() {
+    return (size_t)kWidePts * (32 * 4 * sizeof(uint32_t) + (32 + kWideXch) * sizeof(T)) + 64;
+}
 constexpr int kRevSlots = 16;    // reverse sweep: list entries per lane fetched together
 constexpr uint32_t kRevNone = 0xffffffffu;
 
@@ -61,7 +69,7 @@ struct Table {
     TabParams<T> P{};
     // The table (entries + cell index) and the d/dvals histogram do not fit the LDS budget: the
     // per-point kernels then read the table from global memory and accumulate the histogram
-    // with f64 atomics into their own global row (every k runs on the wavefront-per-point
+    // with f64 atomics into their own global row (every k runs on the group-per-point
     // kernels, which have this form).
     bool global = false;
     std::vector<T> bins, vals;  // host copies
@@ -90,7 +98,7 @@ struct PointK {
     static void sweep_rev(const Graph& g, T* vb, const T* vbar, T* xg, const T* mv, const T* sd,
                           T* xout, const int32_t* oidx, hipStream_t st);
 };
-// The same launchers for any k <= 31 (wavefront-per-point kernels, ggp_wide.h).
+// The same launchers for any k <= 31 (group-per-point kernels, ggp_wide.h).
 template <typename T>
 struct WideK {
     static void factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
@@ -136,8 +144,14 @@ extern template struct WideD<float, 4>;
 extern template struct WideD<double, 2>;
 extern template struct WideD<double, 3>;
 extern template struct WideD<double, 4>;
-constexpr int kMaxK = 31;  // largest neighbour count (wavefront-per-point path)
+constexpr int kMaxK = 31;  // largest neighbour count (group-per-point path)
 inline bool register_block_k(int64_t k) { return k == 4 || k == 8 || k == 10 || k == 16; }
+// LDS the per-point kernels of neighbour count k need beside the table and the histogram: the
+// reductions, and for the group-per-point kernels their per-point areas.
+template <typename T>
+inline size_t lds_slack(int64_t k) {
+    return register_block_k(k) ? 512 + (size_t)4 * 2 * 64 * sizeof(T) : 512 + wide_static_lds<T>();
+}
 
 extern template struct PointK<float, 4>;
 extern template struct PointK<float, 8>;

@@ -85,7 +85,7 @@ __global__ void k_copy(T* __restrict__ dst, const T* __restrict__ src, int64_t n
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) dst[i] = src[i];
 }
-// ---- the wavefront-per-point path (k not in the register-block set) ---------------------------
+// ---- the group-per-point path (k not in the register-block set) ---------------------------
 template <typename T>
 void WideK<T>::factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,
                       double* partial, const T* values, T* xi_out, unsigned nblk,
@@ -131,7 +131,7 @@ static inline unsigned grid_for(int64_t n, int block = kBlock) {
     return (unsigned)((n + block - 1) / block);
 }
 
-// K = 0 selects the wavefront-per-point kernels (every other k up to kMaxK).
+// K = 0 selects the group-per-point kernels (every other k up to kMaxK).
 template <typename T, int K> struct LaunchSel { using type = PointK<T, K>; };
 template <typename T> struct LaunchSel<T, 0> { using type = WideK<T>; };
 template <typename T, int K> using Launch = typename LaunchSel<T, K>::type;
@@ -147,7 +147,7 @@ template <typename T, int K> using Launch = typename LaunchSel<T, K>::type;
         }                                            \
     } while (0)
 
-// A table in global memory (too large for LDS) runs on the wavefront-per-point kernels for
+// A table in global memory (too large for LDS) runs on the group-per-point kernels for
 // every k: they have the global-table form, and give the same IEEE results.
 template <typename T>
 void launch_factor(const Graph& g, const Table<T>& tb, int mode, T* mv, T* sd, T* terms,

@@ -1,4 +1,4 @@
-// ggp_wide.hip — launchers of the wavefront-per-point kernels (any k <= 31), compiled once per
+// ggp_wide.hip — launchers of the group-per-point kernels (any k <= 31), compiled once per
 // (element type, dimension, part): -DGGP_T=<float|double> -DGGP_D=<2|3|4> -DGGP_PART=<0|1|2>
 // (0: the factor pass; 1: the pullback with the table in LDS; 2: the pullback with the table in
 // global memory), so the heavy instantiations build in parallel.
@@ -11,7 +11,7 @@
 namespace ggp {
 
 static inline unsigned grid_wide(int64_t M, unsigned nblk) {
-    const int64_t need = (M + kWideWaves - 1) / kWideWaves;
+    const int64_t need = (M + kWidePts - 1) / kWidePts;
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>((int64_t)nblk, need));
 }
 

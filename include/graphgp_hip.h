@@ -50,7 +50,7 @@ enum {
 const char* ggp_last_error(void);
 
 /* Supported neighbour counts k and dimensions D: 1 <= k <= 31, D in {2, 3, 4}. k in {4, 8, 10,
- * 16} run on register-block kernels (a lane per point), every other k on wavefront-per-point
+ * 16} run on register-block kernels (a lane per point), every other k on group-per-point
  * kernels; the results are the same IEEE operations either way (csrc/graphgp_capi.cu:52-68
  * dispatches k to compiled bounds up to 64). Returns 0, GGP_ERR_K or GGP_ERR_D. */
 int ggp_supported(int64_t k, int32_t D);

@@ -3,7 +3,7 @@
 The reference's lookups take any nbins (src/interp.jl:10-34) and its gradients fall back from the
 shared-memory histogram to global atomics above 2048 bins (src/grad.jl:107-116,
 src/kernels_adjoint.jl:327-424). Here such a table stays in global memory: every k runs on the
-wavefront-per-point kernels, which read it there and accumulate d/dvals with f64 atomics into
+group-per-point kernels, which read it there and accumulate d/dvals with f64 atomics into
 per-workgroup rows. Every op is compared with the oracle at 1e-5 (f32) / 1e-12 (f64)
 L2-relative, forward ops bit for bit; the measured error is printed.
 """

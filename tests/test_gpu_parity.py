@@ -78,7 +78,7 @@ def _check_scalar(name, got, want, bar):
 DTYPES = [np.float32, np.float64]
 SYNTH = [(4000, 2, 100, 4), (4000, 3, 150, 8), (3000, 3, 120, 10), (3000, 3, 200, 16),
          (3000, 4, 150, 8),
-         # any other k runs on the wavefront-per-point kernels (k = 5, 6, 20 as in
+         # any other k runs on the group-per-point kernels (k = 5, 6, 20 as in
          # test/test_gradients.jl:83, test/test_graph_build.jl:26, test/test_degenerate.jl:10;
          # k = 30 as the k=30 Float64 workload; k = 1 and 31 are the ends of the range)
          (3000, 3, 100, 5), (3000, 2, 100, 6), (2500, 3, 128, 20), (2000, 3, 120, 30),
@@ -128,7 +128,7 @@ def test_refine_forward_bit_exact(gpu, dtype):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("k", [5, 20, 30])
 def test_wide_forward_bit_exact(gpu, k, dtype):
-    """The wavefront-per-point Cholesky reproduces the serial left-looking sums term by term:
+    """The group-per-point Cholesky reproduces the serial left-looking sums term by term:
     refine_inv and refine have the oracle's bits. The logdet terms go through the device and
     host libm log, which are not bit-identical, so they are held to the tolerance."""
     _say(f"case wide_bit_exact k={k} {np.dtype(dtype).name}")
