@@ -16,10 +16,11 @@ constexpr int kWideBlock = 256;  // threads per workgroup of the group-per-point
 constexpr int kWidePts = kWideBlock / 32;  // points per workgroup pass there (32 lanes each)
 constexpr int kWideXch = 144;    // exchange area per point there, in elements of T
 // Static LDS of one workgroup of those kernels: per point its rows' coordinates (32 x 4 words),
-// a seed vector (32 T) and the exchange area; plus the block reduction.
+// the pivots' reciprocals and a seed vector (2 x 32 T) and the exchange area; plus the block
+// reduction.
 template <typename T>
 constexpr size_t wide_static_lds() {
-    return (size_t)kWidePts * (32 * 4 * sizeof(uint32_t) + (32 + kWideXch) * sizeof(T)) + 64;
+    return (size_t)kWidePts * (32 * 4 * sizeof(uint32_t) + (64 + kWideXch) * sizeof(T)) + 64;
 }
 constexpr int kRevSlots = 16;    // reverse sweep: list entries per lane fetched together
 constexpr uint32_t kRevNone = 0xffffffffu;

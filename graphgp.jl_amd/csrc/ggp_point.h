@@ -516,6 +516,35 @@ __device__ inline void chol_pullback(T (&Abar)[N * (N + 1) / 2], T (&Lbar)[N * (
     }
 }
 
+// chol_pullback with each off-diagonal Abar[i][j] handed to pair(i, j, Abar[i][j]) when it is
+// formed instead of stored, and the diagonal into sdiag; the same operations in the same order.
+template <typename T, int N, typename F>
+__device__ inline void chol_pullback_each(T (&Lbar)[N * (N + 1) / 2], const T (&L)[N * (N + 1) / 2],
+                                          const T (&rd)[N - 1], T (&sdiag)[N], F&& pair) {
+#pragma unroll
+    for (int j = N - 1; j >= 0; --j) {
+        const T ljj = L[tri(j, j)];
+#pragma unroll
+        for (int i = N - 1; i >= j + 1; --i) {
+            const T lbij = Lbar[tri(i, j)];
+            const T tbar = div_rcp(lbij, ljj, rd[j]);
+            Lbar[tri(j, j)] -= div_rcp(lbij * L[tri(i, j)], ljj, rd[j]);
+            pair(i, j, tbar);
+#pragma unroll
+            for (int p = 0; p < j; ++p) {
+                Lbar[tri(i, p)] = num<T>::fma(-tbar, L[tri(j, p)], Lbar[tri(i, p)]);
+                Lbar[tri(j, p)] = num<T>::fma(-tbar, L[tri(i, p)], Lbar[tri(j, p)]);
+            }
+        }
+        const T sbar = j < N - 1 ? div_rcp(Lbar[tri(j, j)], T(2) * ljj, rd[j < N - 1 ? j : 0] * T(0.5))
+                                 : Lbar[tri(j, j)] / (T(2) * ljj);
+        sdiag[j] = sbar;
+#pragma unroll
+        for (int p = 0; p < j; ++p)
+            Lbar[tri(j, p)] = num<T>::fma(-(T(2) * sbar), L[tri(j, p)], Lbar[tri(j, p)]);
+    }
+}
+
 // ---- LDS staging of the table -----------------------------------------------------------
 // Cooperative copy of the prepared table (entries + cell index) from global memory into LDS.
 template <typename T>

@@ -345,30 +345,6 @@ k_sweep_rev(T* __restrict__ vb, const T* __restrict__ vbar, T* __restrict__ xg,
 }
 
 // ---- adjoint pullback -----------------------------------------------------------------------
-// Histogram scatter of one point's Abar through the lookup weights (src/kernels_adjoint.jl:47-74).
-template <typename T, int K, int D, bool ONE>
-__device__ inline void scatter_hist(double* hist, const Block<T, K, D>& blk,
-                                    const T (&Abar)[(K + 1) * (K + 2) / 2], T scale,
-                                    const TabEnt<T>* tab, const uint16_t* acc,
-                                    const TabParams<T>& P) {
-    constexpr int N = K + 1;
-    T diag = T(0);
-#pragma unroll
-    for (int a = 0; a < N; ++a) diag += Abar[tri(a, a)];
-    atomicAdd(&hist[0], (double)diag);
-#pragma unroll
-    for (int a = 1; a < N; ++a)
-#pragma unroll
-        for (int b = 0; b < a; ++b) {
-            const T r = radius<T>(sqdist<D>(blk.jc[a], blk.jc[b]), scale);
-            T wlo, whi;
-            const int lo = cov_weights<T, ONE>(r, tab, acc, P, wlo, whi);
-            const T g = Abar[tri(a, b)];
-            atomicAdd(&hist[lo], (double)(g * wlo));
-            atomicAdd(&hist[lo + 1], (double)(g * whi));
-        }
-}
-
 // d/dpoints scatter of one point's Abar (src/kernels_adjoint.jl:223-252): each pair's term is
 // summed per block row in double, then one f64 atomic add per row and coordinate into dp
 // (N x D, tree order).
@@ -427,9 +403,9 @@ __device__ inline double pullback_points(const uint32_t* __restrict__ coords,
         blk.template assemble<ONE>(scale, s_tab, s_acc, P);
         blk.cholesky();
         const T s = blk.stddev();
-        T Lbar[NT], Abar[NT];
+        T Lbar[NT];
 #pragma unroll
-        for (int i = 0; i < NT; ++i) { Lbar[i] = T(0); Abar[i] = T(0); }
+        for (int i = 0; i < NT; ++i) Lbar[i] = T(0);
         if (SEED == P_LOGDET) {
             // src/linalg.jl:140-146 with seed 1; the term itself for the fused logdet.
             ssum += (double)num<T>::log(s);
@@ -477,11 +453,28 @@ __device__ inline double pullback_points(const uint32_t* __restrict__ coords,
                 for (int i = 0; i <= j; ++i) Lbar[tri(j, i)] -= zbar[i] * x[j];
             }
         }
-        chol_pullback<T, N>(Abar, Lbar, blk.A, blk.rd);
-        if (PTS)
+        if (PTS) {
+            T Abar[NT];
+#pragma unroll
+            for (int i = 0; i < NT; ++i) Abar[i] = T(0);
+            chol_pullback<T, N>(Abar, Lbar, blk.A, blk.rd);
             scatter_pts<T, K, D, ONE>(hist_partial, blk, nb, m, n0, Abar, scale, s_tab, s_acc, P);
-        else
-            scatter_hist<T, K, D, ONE>(s_hist, blk, Abar, scale, s_tab, s_acc, P);
+        } else {
+            // Abar[i][j] goes through the lookup weights as it is formed (src/kernels_adjoint.jl:
+            // 47-74); the diagonal, summed in row order, into bin 0
+            T sdiag[N];
+            chol_pullback_each<T, N>(Lbar, blk.A, blk.rd, sdiag, [&](int i, int j, T g) {
+                const T r = radius<T>(sqdist<D>(blk.jc[i], blk.jc[j]), scale);
+                T wlo, whi;
+                const int lo = cov_weights<T, ONE>(r, s_tab, s_acc, P, wlo, whi);
+                atomicAdd(&s_hist[lo], (double)(g * wlo));
+                atomicAdd(&s_hist[lo + 1], (double)(g * whi));
+            });
+            T diag = T(0);
+#pragma unroll
+            for (int a = 0; a < N; ++a) diag += sdiag[a];
+            atomicAdd(&s_hist[0], (double)diag);
+        }
     }
     return ssum;
 }

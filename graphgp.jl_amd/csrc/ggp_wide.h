@@ -149,9 +149,11 @@ __device__ __forceinline__ void grp_assemble(T (&a)[kGrp], const uint32_t (&x)[D
 }
 
 // chol_lower! (src/linalg.jl:38-73) on the rows of the group; xv: the group's exchange area.
-// Returns L[31][31] (the point's conditional standard deviation), group-uniform.
+// rd (LDS): RN(1 / L[j][j]) by column, with which the column and every later division by L[j][j]
+// take div_rcp (the IEEE quotient). Returns L[31][31] (the point's conditional standard
+// deviation), group-uniform.
 template <typename T>
-__device__ __forceinline__ T grp_cholesky(T (&a)[kGrp], T* xv, int K, int r, bool hi) {
+__device__ __forceinline__ T grp_cholesky(T (&a)[kGrp], T* xv, T* rd, int K, int r, bool hi) {
     const T pivmin = num<T>::eps() * gbcast(a[0], 0, hi);
     const T dmin = num<T>::sqrt(pivmin);
     T col[kGrp];
@@ -161,7 +163,9 @@ __device__ __forceinline__ T grp_cholesky(T (&a)[kGrp], T* xv, int K, int r, boo
             const T s = gbcast(a[j], j, hi);
             const bool ok = s > pivmin;  // false for NaN, as in the reference
             const T d = ok ? num<T>::sqrt(s) : dmin;
-            const T q = a[j] / d;
+            const T y = T(1) / d;
+            if (r == 0) rd[j] = y;
+            const T q = div_rcp(a[j], d, y);
             a[j] = r == j ? d : (r > j ? (ok ? q : T(0)) : a[j]);
             if (j < kGrpPt) {
                 xv[r] = a[j];
@@ -183,7 +187,7 @@ __device__ __forceinline__ T grp_cholesky(T (&a)[kGrp], T* xv, int K, int r, boo
 // optional): every x_i by index (0 for the padding rows).
 template <typename T>
 __device__ __forceinline__ T grp_mean_vec(const T (&a)[kGrp], int K, int r, bool hi, T* xv,
-                                          T* xs_out) {
+                                          const T* rd, T* xs_out) {
     const T pivfloor = T(1.5) * num<T>::sqrt(num<T>::eps()) * gbcast(a[0], 0, hi);
     T xs[kGrp - 1];
     T col[kGrp];
@@ -200,7 +204,7 @@ __device__ __forceinline__ T grp_mean_vec(const T (&a)[kGrp], int K, int r, bool
             for (int j = 0; j < kGrp - 1; ++j)
                 if (j > i) s = num<T>::fma(-col[j], xs[j], s);
             const T d = col[i];
-            xi = d > pivfloor ? s / d : T(0);
+            xi = d > pivfloor ? div_rcp(s, d, rd[i]) : T(0);
             mine = r == i ? xi : mine;
             __builtin_amdgcn_wave_barrier();
         }
@@ -215,7 +219,8 @@ __device__ __forceinline__ T grp_mean_vec(const T (&a)[kGrp], int K, int r, bool
 // GUARD: zero where the pivot is at the clamp floor (as mean_vec_solve! does). Lane i receives
 // zbar_i.
 template <typename T, bool GUARD>
-__device__ __forceinline__ T grp_zbar(const T (&a)[kGrp], T z0, int K, int r, bool hi) {
+__device__ __forceinline__ T grp_zbar(const T (&a)[kGrp], T z0, int K, int r, bool hi,
+                                      const T* rd) {
     const T pivfloor = T(1.5) * num<T>::sqrt(num<T>::eps()) * gbcast(a[0], 0, hi);
     T zs[kGrp - 1];
     T zm = T(0);
@@ -229,7 +234,8 @@ __device__ __forceinline__ T grp_zbar(const T (&a)[kGrp], T z0, int K, int r, bo
                 if (p < i) t = t - a[p] * zs[p];
             const T ti = gbcast(t, i, hi);
             const T dii = gbcast(a[i], i, hi);
-            zi = GUARD ? (dii > pivfloor ? ti / dii : T(0)) : ti / dii;
+            const T q = div_rcp(ti, dii, rd[i]);
+            zi = GUARD ? (dii > pivfloor ? q : T(0)) : q;
             zm = r == i ? zi : zm;
         }
         zs[i] = zi;
@@ -273,6 +279,7 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ double s_red[kWideWaves];
     __shared__ __align__(16) uint32_t s_xc[kWidePts][kGrp * 4];
+    __shared__ __align__(16) T s_rd[kWidePts][kGrp];
     __shared__ __align__(16) T s_xv[kWidePts][kWideXch];
     TabParams<T> P{};
     TabEnt<T>* s_tab = nullptr;
@@ -294,6 +301,7 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
     const bool hi = lane >= kGrp;
     const int grp = threadIdx.x >> 5;
     uint32_t* xc = s_xc[grp];
+    T* rd = s_rd[grp];
     T* xv = s_xv[grp];
     double lsum = 0.0;
     const int64_t stride = (int64_t)gridDim.x * kWidePts;
@@ -304,7 +312,7 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
         const int32_t nb = grp_gather<D>(x, xc, coords, nbr, M, m, n0, K, r, nbr64);
         T a[kGrp];
         grp_assemble<T, D, ANISO>(a, x, xc, K, r, scale, s_tab, s_acc, P, av);
-        const T s = grp_cholesky(a, xv, K, r, hi);
+        const T s = grp_cholesky(a, xv, rd, K, r, hi);
         if (mode & F_TERMS) {
             const T t = num<T>::log(s);
             if (live && r == 0) {
@@ -313,7 +321,7 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
             }
         }
         if (mode & (F_MV | F_INV)) {
-            const T xm = grp_mean_vec(a, K, r, hi, xv, (T*)nullptr);
+            const T xm = grp_mean_vec(a, K, r, hi, xv, rd, (T*)nullptr);
             if (mode & F_MV) {
                 if (live && r < K) mv[m * K + r] = xm;
                 if (live && r == 0) sd[m] = s;
@@ -361,7 +369,7 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
                         : reinterpret_cast<double*>(smem + tab_bytes<T>(P.nb, P.ucells));
     __shared__ double s_red[kWideWaves];
     __shared__ __align__(16) uint32_t s_xc[kWidePts][kGrp * 4];
-    __shared__ __align__(16) T s_sv[kWidePts][kGrp];
+    __shared__ __align__(16) T s_sv[kWidePts][2 * kGrp];
     __shared__ __align__(16) T s_xv[kWidePts][kWideXch];
     if (!TG) {
         if (!PTS)
@@ -373,7 +381,8 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
     const bool hi = lane >= kGrp;
     const int grp = threadIdx.x >> 5;
     uint32_t* xc = s_xc[grp];
-    T* xs = s_sv[grp];  // seeds: x (mean vector); the loop: sbar by row
+    T* xs = s_sv[grp];         // seeds: x (mean vector); the loop: sbar by row
+    T* rd = s_sv[grp] + kGrp;  // RN(1 / L[j][j]) by column
     T* xv = s_xv[grp];
     const AnisoArgs<T> no_aniso{};
     double ssum = 0.0;
@@ -385,7 +394,7 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
         const int32_t nb = grp_gather<D>(x, xc, coords, nbr, M, m, n0, K, r, nullptr);
         T a[kGrp];
         grp_assemble<T, D, false>(a, x, xc, K, r, scale, s_tab, s_acc, P, no_aniso);
-        const T s = grp_cholesky(a, xv, K, r, hi);
+        const T s = grp_cholesky(a, xv, rd, K, r, hi);
 
         // ---- seeds: bc[i] = Lbar[i][r] ----
         T lc[kGrp], bc[kGrp];
@@ -398,7 +407,7 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
             for (int i = 0; i < kGrp; ++i) bc[i] = T(0);
             bc[kGrpPt] = r == kGrpPt ? seed : T(0);
         } else {
-            const T xm = grp_mean_vec(a, K, r, hi, xv, xs);
+            const T xm = grp_mean_vec(a, K, r, hi, xv, rd, xs);
             const T vnb = r < K ? v[nb] : T(0);
             T seed, z0;
             if (SEED == P_INVLOSS) {
@@ -422,8 +431,8 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
                 z0 = vbp * vnb;
             }
             // unguarded for the inverse loss, guarded like mean_vec_solve! for generate_grad_vals
-            const T zm = SEED == P_INVLOSS ? grp_zbar<T, false>(a, z0, K, r, hi)
-                                           : grp_zbar<T, true>(a, z0, K, r, hi);
+            const T zm = SEED == P_INVLOSS ? grp_zbar<T, false>(a, z0, K, r, hi, rd)
+                                           : grp_zbar<T, true>(a, z0, K, r, hi, rd);
             grp_columns(a, lc, xv, r);
             wave_sync_lds();
             T xsv[kGrp];
@@ -455,12 +464,12 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
                     }
                 }
                 wave_sync_lds();
-                const T lbjj = pb[j], ljj = pl[j];
+                const T lbjj = pb[j], ljj = pl[j], y = rd[j];
                 const bool row = r > j && real_r;
                 const T lb = row ? pb[r] : T(0);
                 const T lij = row ? pl[r] : T(0);
-                const T tbar = lb / ljj;
-                const T qv = lb * lij / ljj;
+                const T tbar = div_rcp(lb, ljj, y);
+                const T qv = div_rcp(lb * lij, ljj, y);
                 // Abar[r][j] = tbar through the lookup weights (src/kernels_adjoint.jl:47-74), or
                 // through k'(r) dr/dx into points r and j (src/kernels_adjoint.jl:223-252)
                 uint32_t xj[D];
@@ -496,7 +505,7 @@ k_pullback_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nb
                         bc[j] = num<T>::fma(-tb, lc[i], bc[j]);  // Lbar[j][r], r < j
                     }
                 }
-                const T sbar = t / (T(2) * ljj);
+                const T sbar = div_rcp(t, T(2) * ljj, y * T(0.5));
                 if (r == 0) xs[j] = sbar;
                 bc[j] = num<T>::fma(-(T(2) * sbar), lc[j], bc[j]);
                 __builtin_amdgcn_wave_barrier();
