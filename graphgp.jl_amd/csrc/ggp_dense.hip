@@ -240,7 +240,7 @@ __global__ void __launch_bounds__(kDfThreads) k_potrf_tiles(T* __restrict__ A, i
 // tasks of earlier groups (or earlier in its own group) and for walker steps <= g, and walker
 // step j waits only for groups <= j-1, so the launch cannot deadlock whatever the residency.
 template <typename T>
-__device__ inline void walk_load(T (&acc)[4], const T* A, int n, int i, int j, int r0, int c) {
+__device__ __forceinline__ void walk_load(T (&acc)[4], const T* A, int n, int i, int j, int r0, int c) {
     const int i0 = i * kTile, j0 = j * kTile;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -252,7 +252,7 @@ __device__ inline void walk_load(T (&acc)[4], const T* A, int n, int i, int j, i
 
 // acc[q] -= X[r0+8q][:] . Y[c][:] over the 32 columns, in column order.
 template <typename T>
-__device__ inline void walk_term(T (&acc)[4], const T (*X)[kTile + 1], const T (*Y)[kTile + 1],
+__device__ __forceinline__ void walk_term(T (&acc)[4], const T (*X)[kTile + 1], const T (*Y)[kTile + 1],
                                  int r0, int c) {
 #pragma unroll 8
     for (int p = 0; p < kTile; ++p) {
@@ -264,7 +264,7 @@ __device__ inline void walk_term(T (&acc)[4], const T (*X)[kTile + 1], const T (
 
 // Terms k in [k0, k1) of tile (i, j) from the published tiles (i, k) and (j, k).
 template <typename T>
-__device__ inline void walk_accumulate(T (&acc)[4], const T* A, int n, int nt, int i, int j,
+__device__ __forceinline__ void walk_accumulate(T (&acc)[4], const T* A, int n, int nt, int i, int j,
                                        int k0, int k1, const int* flags, int* info,
                                        T (*sA)[kTile + 1], T (*sB)[kTile + 1], int tid, int r0,
                                        int c) {
@@ -298,7 +298,7 @@ template <typename T> constexpr bool kRsqFactor = false;
 // Solve the tile in sA against L (row r on lane r of wave 0) into global tile (i, j) and, if
 // out is given, into out (LDS). Called by wave 0.
 template <typename T>
-__device__ inline void walk_solve(T* A, int n, int i, int j, const T (*sA)[kTile + 1],
+__device__ __forceinline__ void walk_solve(T* A, int n, int i, int j, const T (*sA)[kTile + 1],
                                   const T (*L)[kTile + 1], const T* inv, T (*out)[kTile + 1],
                                   int tid) {
     constexpr bool kRsq = kRsqFactor<T>;
@@ -348,7 +348,7 @@ __host__ __device__ inline int dense_sync_flag_ints(int nt) { return (nt * nt + 
 // column-to-column chain; rsq then goes to inv (LDS) and dinv (global, for the helpers' solves).
 // Called by wave 0.
 template <typename T>
-__device__ inline void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1],
+__device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1],
                                      T (*Lt)[kLtPitch], T* inv, T* dinv, T (*col)[kTile],
                                      int tid, int* info) {
     constexpr bool kRsq = kRsqFactor<T>;
@@ -407,7 +407,7 @@ __device__ inline void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1
 // updates; column p of L is a row of Lt (LDS broadcast). The result goes to global tile (i, j)
 // and to P.
 template <typename T>
-__device__ inline void walk_solve_t(T* A, int n, int i, int j, const T (*sC)[kTile + 1],
+__device__ __forceinline__ void walk_solve_t(T* A, int n, int i, int j, const T (*sC)[kTile + 1],
                                     const T (*Lt)[kLtPitch], const T* inv, T (*P)[kTile + 1],
                                     int tid) {
     constexpr bool kRsq = kRsqFactor<T>;
@@ -444,7 +444,7 @@ __device__ inline void walk_solve_t(T* A, int n, int i, int j, const T (*sC)[kTi
 
 // Rows [R, R+16) of tile (i, j) for a 64-lane wavefront: lane l holds (R + (l >> 5) + 2q, l & 31).
 template <typename T>
-__device__ inline void walk_load16(T (&v)[8], const T* A, int n, int i, int j, int R, int lane) {
+__device__ __forceinline__ void walk_load16(T (&v)[8], const T* A, int n, int i, int j, int R, int lane) {
     const int c = lane & (kTile - 1), rr = lane >> 5;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -456,7 +456,7 @@ __device__ inline void walk_load16(T (&v)[8], const T* A, int n, int i, int j, i
 
 // sync: the layout above (dense_sync_flag_ints).
 template <typename T>
-__global__ void __launch_bounds__(kDfThreads) k_potrf_walk(T* __restrict__ A, int n, int nt,
+__global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 4 ? 2 : 1))) k_potrf_walk(T* __restrict__ A, int n, int nt,
                                                            int ntasks, int* __restrict__ sync,
                                                            int* __restrict__ info) {
     __shared__ T sA[kTile][kTile + 1];

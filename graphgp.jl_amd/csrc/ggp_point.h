@@ -289,11 +289,12 @@ __device__ inline T frac_index(T d, const T* __restrict__ bins, int n,
     return T(lo) + (d - x0) / (x1 - x0);
 }
 
-// The axes and their cell indices copied into LDS at smem (an.lds bytes) by the whole
-// workgroup; returns the view to use (an itself when the axes are not staged).
+// The axes and their cell indices copied into LDS at smem (an.lds bytes, nonzero) by the whole
+// workgroup; returns the view whose axes are there. A caller that branches on an.lds and calls
+// this on one side only keeps each side's pointers in one address space (LDS reads on this
+// side, global reads on the other) instead of generic ones.
 template <typename T>
-__device__ inline AnisoArgs<T> aniso_stage(const AnisoArgs<T>& an, unsigned char* smem) {
-    if (an.lds == 0) return an;
+__device__ inline AnisoArgs<T> aniso_stage_lds(const AnisoArgs<T>& an, unsigned char* smem) {
     AnisoArgs<T> s = an;
     T* sb = reinterpret_cast<T*>(smem);
     T* zb = sb + an.ns;
@@ -311,6 +312,12 @@ __device__ inline AnisoArgs<T> aniso_stage(const AnisoArgs<T>& an, unsigned char
     s.sacc = sacc;
     s.zacc = zacc;
     return s;
+}
+
+// aniso_stage_lds when the axes fit (an.lds != 0), else an itself.
+template <typename T>
+__device__ inline AnisoArgs<T> aniso_stage(const AnisoArgs<T>& an, unsigned char* smem) {
+    return an.lds == 0 ? an : aniso_stage_lds(an, smem);
 }
 
 // Bytes aniso_stage needs: both axes, then both cell indices.

@@ -117,18 +117,19 @@ k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, i
         stage_table(s_tab, s_acc, g_tab, g_acc, P);
     }
 
-    AnisoArgs<T> av{};
-    if (ANISO) av = aniso_stage(an, smem);
-
     double lsum = 0.0;
-    if (ANISO || P.steps <= 1)
+    if (ANISO && an.lds != 0)  // axes staged: their reads are LDS reads
+        lsum = factor_points<T, K, D, MODE, ANISO, true>(coords, nbr, M, n0, scale, s_tab, s_acc,
+                                                         P, mv, sd, terms, values, xi_out,
+                                                         aniso_stage_lds(an, smem), nbr64);
+    else if (ANISO || P.steps <= 1)
         lsum = factor_points<T, K, D, MODE, ANISO, true>(coords, nbr, M, n0, scale, s_tab, s_acc,
                                                          P, mv, sd, terms, values,
-                                                         xi_out, av, nbr64);
+                                                         xi_out, an, nbr64);
     else
         lsum = factor_points<T, K, D, MODE, ANISO, false>(coords, nbr, M, n0, scale, s_tab, s_acc,
                                                           P, mv, sd, terms, values,
-                                                          xi_out, av, nbr64);
+                                                          xi_out, an, nbr64);
     if (MODE & F_TERMS) {
         const double t = block_sum(lsum, s_red);
         if (threadIdx.x == 0) partial[blockIdx.x] = t;
