@@ -34,25 +34,31 @@ __global__ void k_dense_assemble(T* __restrict__ A, const uint32_t* __restrict__
     }
     if (blockIdx.x > blockIdx.y) return;  // the whole block lies above the diagonal
     extern __shared__ __align__(16) unsigned char smem[];
-    AnisoArgs<T> av{};
-    if (ANISO) av = aniso_stage(an, smem);  // the whole workgroup, before any return
     const int j = blockIdx.x * 16 + threadIdx.x;
     const int i = blockIdx.y * 16 + threadIdx.y;
-    if (i >= n || j > i) return;
     TabParams<T> P{};
     if (!ANISO) P = *Pp;
-    if (i == j) {
-        const T d0 = ANISO ? aniso_lookup(T(0), T(0), av) : P.v0;
-        A[(int64_t)i * n + i] = diag_add == T(0) ? d0 : d0 + diag_add;
-        return;
-    }
-    uint32_t ci[D], cj[D];
+    auto entry = [&](const AnisoArgs<T>& av) {
+        if (i >= n || j > i) return;
+        if (i == j) {
+            const T d0 = ANISO ? aniso_lookup(T(0), T(0), av) : P.v0;
+            A[(int64_t)i * n + i] = diag_add == T(0) ? d0 : d0 + diag_add;
+            return;
+        }
+        uint32_t ci[D], cj[D];
 #pragma unroll
-    for (int d = 0; d < D; ++d) { ci[d] = coords[(int64_t)i * D + d]; cj[d] = coords[(int64_t)j * D + d]; }
-    const T v = ANISO ? aniso_pair<T, D>(ci, cj, scale, av)
-                      : cov_lookup(radius<T>(sqdist<D>(ci, cj), scale), tab, acc, P);
-    A[(int64_t)i * n + j] = v;
-    A[(int64_t)j * n + i] = v;
+        for (int d = 0; d < D; ++d) {
+            ci[d] = coords[(int64_t)i * D + d];
+            cj[d] = coords[(int64_t)j * D + d];
+        }
+        const T v = ANISO ? aniso_pair<T, D>(ci, cj, scale, av)
+                          : cov_lookup(radius<T>(sqdist<D>(ci, cj), scale), tab, acc, P);
+        A[(int64_t)i * n + j] = v;
+        A[(int64_t)j * n + i] = v;
+    };
+    // staged axes (the whole workgroup stages them) are read from LDS on that side only
+    if (ANISO && an.lds != 0) entry(aniso_stage_lds(an, smem));
+    else entry(an);
 }
 
 // ---- tiled Cholesky: one persistent launch ----------------------------------------------------

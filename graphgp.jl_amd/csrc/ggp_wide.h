@@ -295,8 +295,6 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
             stage_table(s_tab, s_acc, g_tab, g_acc, P);
         }
     }
-    AnisoArgs<T> av{};
-    if (ANISO) av = aniso_stage(an, smem);
     const int lane = threadIdx.x & 63, r = lane & (kGrp - 1);
     const bool hi = lane >= kGrp;
     const int grp = threadIdx.x >> 5;
@@ -305,6 +303,7 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
     T* xv = s_xv[grp];
     double lsum = 0.0;
     const int64_t stride = (int64_t)gridDim.x * kWidePts;
+    auto points = [&](const AnisoArgs<T>& av) __attribute__((always_inline)) {
     for (int64_t b = (int64_t)blockIdx.x * kWidePts + 2 * (threadIdx.x >> 6); b < M; b += stride) {
         const bool live = b + hi < M;
         const int64_t m = live ? b + hi : M - 1;
@@ -339,6 +338,10 @@ k_factor_w(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr,
             }
         }
     }
+    };
+    // staged axes (the whole workgroup stages them) are read from LDS on that side only
+    if (ANISO && an.lds != 0) points(aniso_stage_lds(an, smem));
+    else points(an);
     if (mode & F_TERMS) {
         const double t = block_sum(lsum, s_red);
         if (threadIdx.x == 0) partial[blockIdx.x] = t;
