@@ -16,6 +16,7 @@
 
 namespace ggp {
 
+
 static inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
 // ---- assembly (src/dense.jl:15-40) ----------------------------------------------------------
@@ -352,11 +353,13 @@ __host__ __device__ inline int dense_sync_flag_ints(int nt) { return (nt * nt + 
 // one reciprocal square root per column (v_rsq_f32, within 1 ulp), L[p][p] = pivot * rsq and
 // the column multiplied by rsq, which takes the square root and the division off the
 // column-to-column chain; rsq then goes to inv (LDS) and dinv (global, for the helpers' solves).
-// Called by wave 0.
-template <typename T>
+// Called by wave 0. STREAM: row p of Lt is written as column p is finished, and after every
+// fourth column *prog = pbase + p + 1 (LDS, release), so a solve on another wavefront can follow
+// four columns at a time.
+template <typename T, bool STREAM = false>
 __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1],
                                      T (*Lt)[kLtPitch], T* inv, T* dinv, T (*col)[kTile],
-                                     int tid, int* info) {
+                                     int tid, int* info, int* prog = nullptr, int pbase = 0) {
     constexpr bool kRsq = kRsqFactor<T>;
     const int r = tid & (kTile - 1), h = tid >> 5;
     const bool live = j * kTile + r < n;
@@ -384,7 +387,12 @@ __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[
         a[up] = mine ? (r == p ? d : l) : a[up];
         T* cp = col[p & 1];
         if (mine) cp[r] = r > p ? l : T(0);
+        if (STREAM && mine) Lt[p][r] = r > p ? l : (r == p ? d : T(0));
         wave_sync_lds();
+        if (STREAM && (p & 3) == 3) {  // columns released four at a time
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (tid == 0) __hip_atomic_store(prog, pbase + p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
         const T own = cp[r];
         T cv[16];
 #pragma unroll
@@ -401,9 +409,26 @@ __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[
         if (kRsq && diag_lane) dinv[j * kTile + r] = myinv;
     }
     if (kRsq && diag_lane) inv[r] = myinv;
+    if (!STREAM) {
 #pragma unroll
-    for (int u = 0; u < 16; ++u) Lt[16 * h + u][r] = 16 * h + u <= r ? a[u] : T(0);
+        for (int u = 0; u < 16; ++u) Lt[16 * h + u][r] = 16 * h + u <= r ? a[u] : T(0);
+    }
     if (tid == 0 && bad) atomicOr(info, 1);
+}
+
+// Waits, wave-uniformly, until the LDS counter *v reaches target (bounded: past kDfSpinLimit
+// polls bit 1 of *info is set and the wait ends), then orders the later LDS reads after it.
+__device__ __forceinline__ void lds_wait_ge(const int* v, int target, int* info) {
+    int spins = 0;
+    while (__builtin_amdgcn_readfirstlane(
+               __hip_atomic_load(v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < target) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > kDfSpinLimit) {
+            atomicOr(info, 2);
+            break;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
 // Walker solve of X L^T = B (B in sC) by columns: step p divides column p by L[p][p] and folds
@@ -448,6 +473,64 @@ __device__ __forceinline__ void walk_solve_t(T* A, int n, int i, int j, const T 
     for (int u = 0; u < 16; ++u) P[r][16 * h + u] = a[u];
 }
 
+// The walker's solve of the sub-diagonal tile, following walk_factor_t<T, true> on another
+// wavefront: X L^T = B (B in sC) by columns in the row layout, lane r (and its mirror r + 32,
+// which computes the same and stores nothing) holding all 32 entries of row r. Columns come in
+// batches of four: one wait for *prog (pbase + 4b + 4 releases columns 4b .. 4b+3), then the
+// four reciprocals RN(1 / L[p][p]) together, then per column x = B'[r][p] / L[p][p] (div_rcp,
+// the IEEE quotient) folded into the later columns by fma(-x, L[c][p], a[c]) with L[c][p] from
+// row p of Lt (LDS broadcast) — walk_solve_t's chains in its order. The result goes to global
+// tile (i, j) and to P.
+template <typename T>
+__device__ __forceinline__ void walk_solve_stream(T* A, int n, int i, int j,
+                                                  const T (*sC)[kTile + 1],
+                                                  const T (*Lt)[kLtPitch], T (*P)[kTile + 1],
+                                                  int lane, const int* prog, int pbase, int* info) {
+    constexpr int V = 16 / (int)sizeof(T);
+    struct alignas(16) Q { T e[V]; };
+    const int r = lane & (kTile - 1);
+    const bool lo = lane < kTile;
+    T a[kTile];
+#pragma unroll
+    for (int c = 0; c < kTile; ++c) a[c] = sC[r][c];
+#pragma unroll
+    for (int b = 0; b < kTile / 4; ++b) {
+        lds_wait_ge(prog, pbase + 4 * b + 4, info);
+        T dg[4], y[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dg[u] = Lt[4 * b + u][4 * b + u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) y[u] = T(1) / dg[u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int p = 4 * b + u;
+            const T x = div_rcp(a[p], dg[u], y[u]);
+            a[p] = x;
+            T lc[kTile];
+#pragma unroll
+            for (int c0 = 0; c0 < kTile; c0 += V) {
+                if (c0 + V > p + 1) {
+                    const Q q = *reinterpret_cast<const Q*>(&Lt[p][c0]);
+#pragma unroll
+                    for (int e = 0; e < V; ++e) lc[c0 + e] = q.e[e];
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < kTile; ++c)
+                if (c > p) a[c] = num<T>::fma(-x, lc[c], a[c]);
+        }
+    }
+    if (lo) {
+        if (i * kTile + r < n) {
+            T* wp = A + (int64_t)(i * kTile + r) * n + j * kTile;
+#pragma unroll
+            for (int c = 0; c < kTile; ++c) wp[c] = a[c];
+        }
+#pragma unroll
+        for (int c = 0; c < kTile; ++c) P[r][c] = a[c];
+    }
+}
+
 // Rows [R, R+16) of tile (i, j) for a 64-lane wavefront: lane l holds (R + (l >> 5) + 2q, l & 31).
 template <typename T>
 __device__ __forceinline__ void walk_load16(T (&v)[8], const T* A, int n, int i, int j, int R, int lane) {
@@ -469,10 +552,13 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
     __shared__ T sB[kTile][kTile + 1];
     __shared__ T sC[kTile][kTile + 1];
     __shared__ T sP[kTile][kTile + 1];            // walker: L[j][j-1], then L[j+1][j]
+    __shared__ T sA2[kTile][kTile + 1];           // walker: the next diagonal partial sum
+    __shared__ __align__(16) T sBw[kTile][kLtPitch];  // walker: tile (j+1, j-1), aligned rows
     __shared__ __align__(16) T sLt[kTile][kLtPitch];  // walker: L[j][j] transposed
     __shared__ T sInv[kTile];                         // f32: 1 / L[p][p] of the current tile
     __shared__ __align__(16) T sCol[2][kTile];        // walker factor: the published column
     __shared__ int s_task;
+    __shared__ int s_prog, s_subready;  // walker: columns of L[j][j] out; sub-diagonal tiles in
     int* ticket = sync;
     int* flags = sync + 1;
     int* pdf = flags + nt * nt;
@@ -480,83 +566,116 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
     T* dinv = reinterpret_cast<T*>(sync + dense_sync_flag_ints(nt));
     const int tid = threadIdx.x;
     const int c = tid & (kTile - 1), r0 = tid >> 5;
-    if (tid == 0) s_task = atomicAdd(ticket, 1);
+    if (tid == 0) {
+        s_task = atomicAdd(ticket, 1);
+        s_prog = 0;
+        s_subready = 0;
+    }
     __syncthreads();
     int t = __builtin_amdgcn_readfirstlane(s_task);
     if (t == 0) {
         // ---- the walker ----
-        // Wave 0 factors and solves; waves 1 and 2 (rows 0-15 and 16-31) meanwhile prepare the
-        // next sub-diagonal tile and the next diagonal partial sum. The walker is the critical
-        // path and shares its CU with the concurrent per-point kernels: its waves take issue
-        // priority on their SIMDs.
+        // Per step j: wave 0 factors (j, j) and publishes its columns as they are finished;
+        // wave 3 solves (j+1, j) against them a column or two behind; waves 1 and 2 (rows 0-15
+        // and 16-31) first prepare the sub-diagonal tile (j+1, j) for wave 3 and then the next
+        // diagonal partial sum (in the other buffer). The walker is the critical path and
+        // shares its CU with the concurrent per-point kernels: its waves take issue priority on
+        // their SIMDs.
         __builtin_amdgcn_s_setprio(3);
         const int w = tid >> 6, lane = tid & 63;
+        T (*cur)[kTile + 1] = sA;
+        T (*nxt)[kTile + 1] = sA2;
         {
             T v[4];
             walk_load(v, A, n, 0, 0, r0, c);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) sA[r0 + 8 * q][c] = v[q];
+            for (int q = 0; q < 4; ++q) cur[r0 + 8 * q][c] = v[q];
         }
         __syncthreads();
         for (int j = 0; j < nt; ++j) {
             const bool sub = j + 1 < nt;
-            // diagonal tile: partial sum (in sA) plus the k = j-1 term
+            // diagonal tile: partial sum (in cur) plus the k = j-1 term
             T acc[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) acc[q] = sA[r0 + 8 * q][c];
+            for (int q = 0; q < 4; ++q) acc[q] = cur[r0 + 8 * q][c];
             if (j >= 1) walk_term(acc, sP, sP, r0, c);
             __syncthreads();
 #pragma unroll
-            for (int q = 0; q < 4; ++q) sA[r0 + 8 * q][c] = acc[q];
+            for (int q = 0; q < 4; ++q) cur[r0 + 8 * q][c] = acc[q];
             __syncthreads();
             if (w == 0) {
-                walk_factor_t(A, n, j, sA, sLt, sInv, dinv, sCol, tid, info);
+                walk_factor_t<T, true>(A, n, j, cur, sLt, sInv, dinv, sCol, tid, info, &s_prog,
+                                       j * kTile);
+                __hip_atomic_store(&flags[j * nt + j], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
             } else if (sub && w <= 2) {
-                // sub-diagonal tile: partial sum over k < j-1 plus the k = j-1 term, into sC
+                // sub-diagonal tile: partial sum over k < j-1 plus the k = j-1 term, into sC.
+                // Lane (rb, cb) of wave w holds rows R + 4rb .. R + 4rb + 3, columns 2cb, 2cb + 1;
+                // the rows of (j+1, j-1) come from a 16-byte-aligned copy, four terms per read,
+                // every entry's chain in increasing p.
                 const int R = 16 * (w - 1);
-                if (lane == 0) {
-                    if (j >= 2) df_wait(&psf[j], info);
-                    if (j >= 1) df_wait(&flags[(j + 1) * nt + j - 1], info);
-                }
-                T nx[8];
-                walk_load16(nx, A, n, j + 1, j, R, lane);
+                // the partial sum is ready long before the tile (j+1, j-1): load it first
+                if (lane == 0 && j >= 2) df_wait(&psf[j], info);
+                constexpr int V = 16 / (int)sizeof(T);
+                struct alignas(16) Q { T e[V]; };
+                const int rb = lane >> 4, cb = lane & 15;
+                const int row0 = R + 4 * rb, col0 = 2 * cb;
+                T nx[4][2];
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        const int gr = (j + 1) * kTile + row0 + a;
+                        nx[a][b] = gr < n ? A[(int64_t)gr * n + j * kTile + col0 + b] : T(0);
+                    }
+                if (lane == 0 && j >= 1) df_wait(&flags[(j + 1) * nt + j - 1], info);
                 if (j >= 1) {
                     T lo[8];
                     walk_load16(lo, A, n, j + 1, j - 1, R, lane);
 #pragma unroll
-                    for (int q = 0; q < 8; ++q) sB[R + (lane >> 5) + 2 * q][lane & 31] = lo[q];
+                    for (int q = 0; q < 8; ++q) sBw[R + (lane >> 5) + 2 * q][lane & 31] = lo[q];
                     wave_sync_lds();
-#pragma unroll 8
-                    for (int p = 0; p < kTile; ++p) {
-                        const T lc = sP[lane & 31][p];
 #pragma unroll
-                        for (int q = 0; q < 8; ++q)
-                            nx[q] = num<T>::fma(-sB[R + (lane >> 5) + 2 * q][p], lc, nx[q]);
+                    for (int p0 = 0; p0 < kTile; p0 += V) {
+                        Q rv[4];
+#pragma unroll
+                        for (int a = 0; a < 4; ++a) rv[a] = *reinterpret_cast<const Q*>(&sBw[row0 + a][p0]);
+                        T cv[2][V];
+#pragma unroll
+                        for (int b = 0; b < 2; ++b)
+#pragma unroll
+                            for (int u = 0; u < V; ++u) cv[b][u] = sP[col0 + b][p0 + u];
+#pragma unroll
+                        for (int u = 0; u < V; ++u)
+#pragma unroll
+                            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                                for (int b = 0; b < 2; ++b)
+                                    nx[a][b] = num<T>::fma(-rv[a].e[u], cv[b][u], nx[a][b]);
                     }
                 }
 #pragma unroll
-                for (int q = 0; q < 8; ++q) sC[R + (lane >> 5) + 2 * q][lane & 31] = nx[q];
+                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) sC[row0 + a][col0 + b] = nx[a][b];
+                // sC (and the reads of sP above) before wave 3 starts: it overwrites sP
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                if (lane == 0) atomicAdd(&s_subready, 1);
+                // next diagonal partial sum into nxt
+                if (lane == 0 && j + 1 >= 2) df_wait(&pdf[j + 1], info);
+                T v[8];
+                walk_load16(v, A, n, j + 1, j + 1, R, lane);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) nxt[R + (lane >> 5) + 2 * q][lane & 31] = v[q];
+            } else if (sub && w == 3) {
+                lds_wait_ge(&s_subready, 2 * (j + 1), info);
+                walk_solve_stream(A, n, j + 1, j, sC, sLt, sP, lane, &s_prog, j * kTile, info);
+                __hip_atomic_store(&flags[(j + 1) * nt + j], 1, __ATOMIC_RELEASE,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             }
             __syncthreads();
-            if (tid == 0)
-                __hip_atomic_store(&flags[j * nt + j], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-            if (sub) {
-                if (w == 0) {
-                    walk_solve_t(A, n, j + 1, j, sC, sLt, sInv, sP, tid);
-                } else if (w <= 2) {
-                    // next diagonal partial sum into sA
-                    const int R = 16 * (w - 1);
-                    if (lane == 0 && j + 1 >= 2) df_wait(&pdf[j + 1], info);
-                    T v[8];
-                    walk_load16(v, A, n, j + 1, j + 1, R, lane);
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) sA[R + (lane >> 5) + 2 * q][lane & 31] = v[q];
-                }
-                __syncthreads();
-                if (tid == 0)
-                    __hip_atomic_store(&flags[(j + 1) * nt + j], 1, __ATOMIC_RELEASE,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            }
+            T (*tmp)[kTile + 1] = cur;
+            cur = nxt;
+            nxt = tmp;
         }
         return;
     }
