@@ -484,7 +484,7 @@ __device__ __forceinline__ void walk_solve_t(T* A, int n, int i, int j, const T 
 template <typename T>
 __device__ __forceinline__ void walk_solve_stream(T* A, int n, int i, int j,
                                                   const T (*sC)[kTile + 1],
-                                                  const T (*Lt)[kLtPitch], T (*P)[kTile + 1],
+                                                  const T (*Lt)[kLtPitch], T (*P)[kLtPitch],
                                                   int lane, const int* prog, int pbase, int* info) {
     constexpr int V = 16 / (int)sizeof(T);
     struct alignas(16) Q { T e[V]; };
@@ -551,7 +551,7 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
     __shared__ T sA[kTile][kTile + 1];
     __shared__ T sB[kTile][kTile + 1];
     __shared__ T sC[kTile][kTile + 1];
-    __shared__ T sP[kTile][kTile + 1];            // walker: L[j][j-1], then L[j+1][j]
+    __shared__ __align__(16) T sP[kTile][kLtPitch];  // walker: L[j][j-1], then L[j+1][j]
     __shared__ T sA2[kTile][kTile + 1];           // walker: the next diagonal partial sum
     __shared__ __align__(16) T sBw[kTile][kLtPitch];  // walker: tile (j+1, j-1), aligned rows
     __shared__ __align__(16) T sLt[kTile][kLtPitch];  // walker: L[j][j] transposed
@@ -594,15 +594,39 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
         __syncthreads();
         for (int j = 0; j < nt; ++j) {
             const bool sub = j + 1 < nt;
-            // diagonal tile: partial sum (in cur) plus the k = j-1 term
-            T acc[4];
+            // diagonal tile: partial sum (in cur) plus the k = j-1 term; thread (ra, cb) holds
+            // rows 2ra, 2ra+1 and columns 2cb, 2cb+1, the rows of L[j][j-1] read four terms at a
+            // time, every entry's chain in increasing p
+            if (j >= 1) {
+                constexpr int V = 16 / (int)sizeof(T);
+                struct alignas(16) Q { T e[V]; };
+                const int ra = tid >> 4, cb = tid & 15;
+                T acc[2][2];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) acc[q] = cur[r0 + 8 * q][c];
-            if (j >= 1) walk_term(acc, sP, sP, r0, c);
-            __syncthreads();
+                for (int a = 0; a < 2; ++a)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) cur[r0 + 8 * q][c] = acc[q];
-            __syncthreads();
+                    for (int b = 0; b < 2; ++b) acc[a][b] = cur[2 * ra + a][2 * cb + b];
+#pragma unroll
+                for (int p0 = 0; p0 < kTile; p0 += V) {
+                    Q x[2], y[2];
+#pragma unroll
+                    for (int a = 0; a < 2; ++a) x[a] = *reinterpret_cast<const Q*>(&sP[2 * ra + a][p0]);
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) y[b] = *reinterpret_cast<const Q*>(&sP[2 * cb + b][p0]);
+#pragma unroll
+                    for (int u = 0; u < V; ++u)
+#pragma unroll
+                        for (int a = 0; a < 2; ++a)
+#pragma unroll
+                            for (int b = 0; b < 2; ++b)
+                                acc[a][b] = num<T>::fma(-x[a].e[u], y[b].e[u], acc[a][b]);
+                }
+#pragma unroll
+                for (int a = 0; a < 2; ++a)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) cur[2 * ra + a][2 * cb + b] = acc[a][b];
+                __syncthreads();
+            }
             if (w == 0) {
                 walk_factor_t<T, true>(A, n, j, cur, sLt, sInv, dinv, sCol, tid, info, &s_prog,
                                        j * kTile);
