@@ -302,40 +302,18 @@ __device__ __forceinline__ void walk_accumulate(T (&acc)[4], const T* A, int n, 
 // factor's rounding through L^-1, agree with the oracle's to the rounding of their own sums).
 template <typename T> constexpr bool kRsqFactor = false;
 
-// Solve the tile in sA against L (row r on lane r of wave 0) into global tile (i, j) and, if
-// out is given, into out (LDS). Called by wave 0.
-template <typename T>
-__device__ __forceinline__ void walk_solve(T* A, int n, int i, int j, const T (*sA)[kTile + 1],
-                                  const T (*L)[kTile + 1], const T* inv, T (*out)[kTile + 1],
-                                  int tid) {
-    constexpr bool kRsq = kRsqFactor<T>;
-    const int r = tid & (kTile - 1);
-    const bool live = tid < kTile && i * kTile + r < n;
-    T a[kTile];
-#pragma unroll
-    for (int cc = 0; cc < kTile; ++cc) a[cc] = sA[r][cc];
-#pragma unroll
-    for (int jj = 0; jj < kTile; ++jj) {
-        T tt = a[jj];
-#pragma unroll
-        for (int p = 0; p < jj; ++p) tt = num<T>::fma(-a[p], L[jj][p], tt);
-        a[jj] = kRsq ? tt * inv[jj] : tt / L[jj][jj];
-    }
-    if (live) {
-        T* wp = A + (int64_t)(i * kTile + r) * n + j * kTile;
-#pragma unroll
-        for (int cc = 0; cc < kTile; ++cc) wp[cc] = a[cc];
-    }
-    if (out && tid < kTile)
-#pragma unroll
-        for (int cc = 0; cc < kTile; ++cc) out[r][cc] = a[cc];
-}
-
 __host__ __device__ inline int walk_group_tasks(int g, int nt) {
     return std::max(0, nt - g - 2) + (g + 2 < nt ? 1 : 0) + (g + 3 < nt ? 1 : 0);
 }
 
 constexpr int kLtPitch = kTile + 4;  // transposed L rows, 16-byte aligned
+
+// Position of row c of L in a row of the tile solves' transposed L (G lanes per row, lane g
+// holding columns g, g + G, ...): the columns of lane g are contiguous.
+template <int G>
+__host__ __device__ constexpr int walk_perm(int c) {
+    return (c % G) * (kTile / G) + c / G;
+}
 
 // sync = [ticket, tile flags[nt*nt], diagonal-partial flags[nt], sub-diagonal-partial flags[nt],
 // (padding to 8 bytes), reciprocal diagonal[nt*kTile] (f32 walker)]: ints before the last part.
@@ -353,9 +331,9 @@ __host__ __device__ inline int dense_sync_flag_ints(int nt) { return (nt * nt + 
 // one reciprocal square root per column (v_rsq_f32, within 1 ulp), L[p][p] = pivot * rsq and
 // the column multiplied by rsq, which takes the square root and the division off the
 // column-to-column chain; rsq then goes to inv (LDS) and dinv (global, for the helpers' solves).
-// Called by wave 0. STREAM: row p of Lt is written as column p is finished, and after every
-// fourth column *prog = pbase + p + 1 (LDS, release), so a solve on another wavefront can follow
-// four columns at a time.
+// Called by wave 0. STREAM: column p of L goes to row p of Lt in the order of walk_perm<4> as
+// it is finished, and after every fourth column *prog = pbase + p + 1 (LDS, release), so the
+// solve walk_solve_grp<T, 4, true> on other wavefronts can follow four columns at a time.
 template <typename T, bool STREAM = false>
 __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1],
                                      T (*Lt)[kLtPitch], T* inv, T* dinv, T (*col)[kTile],
@@ -387,7 +365,7 @@ __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[
         a[up] = mine ? (r == p ? d : l) : a[up];
         T* cp = col[p & 1];
         if (mine) cp[r] = r > p ? l : T(0);
-        if (STREAM && mine) Lt[p][r] = r > p ? l : (r == p ? d : T(0));
+        if (STREAM && mine) Lt[p][walk_perm<4>(r)] = r > p ? l : (r == p ? d : T(0));
         wave_sync_lds();
         if (STREAM && (p & 3) == 3) {  // columns released four at a time
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -417,117 +395,126 @@ __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[
 }
 
 // Waits, wave-uniformly, until the LDS counter *v reaches target (bounded: past kDfSpinLimit
-// polls bit 1 of *info is set and the wait ends), then orders the later LDS reads after it.
-__device__ __forceinline__ void lds_wait_ge(const int* v, int target, int* info) {
-    int spins = 0;
-    while (__builtin_amdgcn_readfirstlane(
-               __hip_atomic_load(v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < target) {
+// polls bit 1 of *info is set and the wait ends), then orders the later LDS reads after it;
+// returns the value seen (target after a timeout).
+__device__ __forceinline__ int lds_wait_ge(const int* v, int target, int* info) {
+    int spins = 0, seen;
+    while ((seen = __builtin_amdgcn_readfirstlane(
+                __hip_atomic_load(v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))) < target) {
         __builtin_amdgcn_s_sleep(1);
         if (++spins > kDfSpinLimit) {
             atomicOr(info, 2);
+            seen = target;
             break;
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    return seen;
 }
 
-// Walker solve of X L^T = B (B in sC) by columns: step p divides column p by L[p][p] and folds
-// it into the later columns, so entry (r, c) receives fma(-x[r][p], L[c][p], .) for p = 0, 1,
-// ... and then its division: the row-by-row substitution's chain, in its order. Wave 0; lane
-// 32h + r holds row r, columns 16h .. 16h+15, so both halves of the wavefront share the
-// updates; column p of L is a row of Lt (LDS broadcast). The result goes to global tile (i, j)
-// and to P.
-template <typename T>
-__device__ __forceinline__ void walk_solve_t(T* A, int n, int i, int j, const T (*sC)[kTile + 1],
-                                    const T (*Lt)[kLtPitch], const T* inv, T (*P)[kTile + 1],
-                                    int tid) {
-    constexpr bool kRsq = kRsqFactor<T>;
-    const int r = tid & (kTile - 1), h = tid >> 5;
-    T a[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) a[u] = sC[r][16 * h + u];
-#pragma unroll
-    for (int p = 0; p < kTile; ++p) {
-        const int hp = p >> 4, up = p & 15;
-        const T x = kRsq ? a[up] * inv[p] : a[up] / Lt[p][p];
-        const bool mine = h == hp;
-        a[up] = mine ? x : a[up];
-        const T xo = __shfl_xor(x, 32, 64);
-        const T xp = mine ? x : xo;
-        const T* lrow = &Lt[p][16 * h];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            // columns past p only: u > p in half 0, u + 16 > p in half 1
-            if (u + 16 > p) {
-                const T y = num<T>::fma(-xp, lrow[u], a[u]);
-                a[u] = (u > p || h == 1) ? y : a[u];
-            }
-        }
-    }
-    if (i * kTile + r < n) {
-        T* wp = A + (int64_t)(i * kTile + r) * n + j * kTile + 16 * h;
-#pragma unroll
-        for (int u = 0; u < 16; ++u) wp[u] = a[u];
-    }
-#pragma unroll
-    for (int u = 0; u < 16; ++u) P[r][16 * h + u] = a[u];
+
+// ---- tile solves X L^T = B with G lanes per row ----
+// Lane g of a row's group holds the row's columns c = G k + g (k < kTile / G). Column p is
+// divided on its lane (g = p mod G) by L[p][p], and the quotient goes to the other lanes of the
+// group by a DPP broadcast (quad_perm for G <= 4; for G = 8, row_newbcast into each half of a
+// 16-lane row), after which every later column of the row takes fma(-x, L[c][p], .): each
+// entry receives the row-by-row substitution's terms in its order, then its division, which is
+// div_rcp with RN(1 / L[c][c]) (the IEEE quotient). L comes transposed and permuted:
+// Lp[p][walk_perm<G>(c)] = L[c][p], zero for c < p, so a lane's values of column p are
+// 16-byte aligned and contiguous.
+template <int G, int O>
+constexpr int walk_qsel() {
+    int s = 0;
+    for (int q = 0; q < 4; ++q) s |= ((q & ~(G - 1)) | O) << (2 * q);
+    return s;
 }
 
-// The walker's solve of the sub-diagonal tile, following walk_factor_t<T, true> on another
-// wavefront: X L^T = B (B in sC) by columns in the row layout, lane r (and its mirror r + 32,
-// which computes the same and stores nothing) holding all 32 entries of row r. Columns come in
-// batches of four: one wait for *prog (pbase + 4b + 4 releases columns 4b .. 4b+3), then the
-// four reciprocals RN(1 / L[p][p]) together, then per column x = B'[r][p] / L[p][p] (div_rcp,
-// the IEEE quotient) folded into the later columns by fma(-x, L[c][p], a[c]) with L[c][p] from
-// row p of Lt (LDS broadcast) — walk_solve_t's chains in its order. The result goes to global
-// tile (i, j) and to P.
-template <typename T>
-__device__ __forceinline__ void walk_solve_stream(T* A, int n, int i, int j,
-                                                  const T (*sC)[kTile + 1],
-                                                  const T (*Lt)[kLtPitch], T (*P)[kLtPitch],
-                                                  int lane, const int* prog, int pbase, int* info) {
+// The value of lane O of each G-lane group, for every lane of the group.
+template <int G, int O>
+__device__ __forceinline__ int walk_gbcast(int x) {
+    static_assert(G == 2 || G == 4 || G == 8, "groups of 2, 4 or 8 lanes");
+    if constexpr (G <= 4) {
+        return __builtin_amdgcn_update_dpp(0, x, walk_qsel<G, O>(), 0xf, 0xf, false);
+    } else {
+        // row_newbcast:n (DPP control 0x150 + n): lane n of the 16-lane row; bank mask 0x3
+        // writes lanes 0-7 of the row, 0xc lanes 8-15
+        const int lo = __builtin_amdgcn_update_dpp(0, x, 0x150 + O, 0xf, 0x3, false);
+        return __builtin_amdgcn_update_dpp(lo, x, 0x158 + O, 0xf, 0xc, false);
+    }
+}
+template <int G, int O>
+__device__ __forceinline__ float walk_gbcast(float x) {
+    return __int_as_float(walk_gbcast<G, O>(__float_as_int(x)));
+}
+template <int G, int O>
+__device__ __forceinline__ double walk_gbcast(double x) {
+    const long long v = __double_as_longlong(x);
+    const int lo = walk_gbcast<G, O>((int)(v & 0xffffffffLL));
+    const int hi = walk_gbcast<G, O>((int)(v >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// Solves X L^T = B for the 32 x 32 tile B in sX into global tile (i, j) (rows below n) and, if P
+// is given, into P. Threads gt = 0 .. 32 G - 1 take part: lane (gt & 63) of wavefront gt >> 6
+// holds row (gt >> 6) * (64 / G) + (gt & 63) / G. STREAM (G = 4): the columns of L arrive four
+// at a time from walk_factor_t<T, true> on another wavefront; before column p = 4b a wavefront
+// that has not yet seen *prog >= pbase + 4b + 4 waits for it.
+template <typename T, int G, bool STREAM>
+__device__ __forceinline__ void walk_solve_grp(T* A, int n, int i, int j, const T (*sX)[kTile + 1],
+                                               const T (*Lp)[kLtPitch], T (*P)[kLtPitch], int gt,
+                                               const int* prog, int pbase, int* info) {
+    static_assert(!kRsqFactor<T>, "the division by L[p][p] is the IEEE quotient");
+    static_assert(!STREAM || G == 4, "a streamed batch of four columns is one k");
+    constexpr int K = kTile / G;
     constexpr int V = 16 / (int)sizeof(T);
     struct alignas(16) Q { T e[V]; };
-    const int r = lane & (kTile - 1);
-    const bool lo = lane < kTile;
-    T a[kTile];
+    const int lane = gt & 63, g = lane & (G - 1);
+    const int r = (gt >> 6) * (64 / G) + lane / G;
+    T a[K], dv[K], yv[K];
 #pragma unroll
-    for (int c = 0; c < kTile; ++c) a[c] = sC[r][c];
+    for (int k = 0; k < K; ++k) a[k] = sX[r][G * k + g];
+    if constexpr (!STREAM) {
 #pragma unroll
-    for (int b = 0; b < kTile / 4; ++b) {
-        lds_wait_ge(prog, pbase + 4 * b + 4, info);
-        T dg[4], y[4];
+        for (int k = 0; k < K; ++k) dv[k] = Lp[G * k + g][g * K + k];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) dg[u] = Lt[4 * b + u][4 * b + u];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) y[u] = T(1) / dg[u];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int p = 4 * b + u;
-            const T x = div_rcp(a[p], dg[u], y[u]);
-            a[p] = x;
-            T lc[kTile];
-#pragma unroll
-            for (int c0 = 0; c0 < kTile; c0 += V) {
-                if (c0 + V > p + 1) {
-                    const Q q = *reinterpret_cast<const Q*>(&Lt[p][c0]);
-#pragma unroll
-                    for (int e = 0; e < V; ++e) lc[c0 + e] = q.e[e];
-                }
-            }
-#pragma unroll
-            for (int c = 0; c < kTile; ++c)
-                if (c > p) a[c] = num<T>::fma(-x, lc[c], a[c]);
-        }
+        for (int k = 0; k < K; ++k) yv[k] = T(1) / dv[k];
     }
-    if (lo) {
-        if (i * kTile + r < n) {
-            T* wp = A + (int64_t)(i * kTile + r) * n + j * kTile;
-#pragma unroll
-            for (int c = 0; c < kTile; ++c) wp[c] = a[c];
+    T piv = a[0];  // on lane p mod G: column p, all earlier terms in
+    int avail = 0;  // STREAM: columns of L seen to be out (a wait only when past them)
+    static_for<0, kTile>([&](auto PI) __attribute__((always_inline)) {
+        constexpr int p = decltype(PI)::value;
+        constexpr int go = p % G, ko = p / G;
+        if constexpr (STREAM && p % 4 == 0) {
+            if (avail < p + 4) avail = lds_wait_ge(prog, pbase + p + 4, info) - pbase;
+            dv[ko] = Lp[p + g][g * K + ko];
+            yv[ko] = T(1) / dv[ko];
         }
+        const T x = div_rcp(piv, dv[ko], yv[ko]);
+        const T xb = walk_gbcast<G, go>(x);
+        T lc[K];
 #pragma unroll
-        for (int c = 0; c < kTile; ++c) P[r][c] = a[c];
+        for (int k0 = 0; k0 < K; k0 += V) {
+            if (k0 + V > ko) {
+                const Q q = *reinterpret_cast<const Q*>(&Lp[p][g * K + k0]);
+#pragma unroll
+                for (int e = 0; e < V; ++e) lc[k0 + e] = q.e[e];
+            }
+        }
+        const T upd = num<T>::fma(-xb, lc[ko], a[ko]);
+        a[ko] = g == go ? x : (g > go ? upd : a[ko]);
+#pragma unroll
+        for (int k = ko + 1; k < K; ++k) a[k] = num<T>::fma(-xb, lc[k], a[k]);
+        if constexpr (go + 1 < G) piv = upd;
+        else if constexpr (ko + 1 < K) piv = a[ko + 1];
+    });
+    if (i * kTile + r < n) {
+        T* wp = A + (int64_t)(i * kTile + r) * n + j * kTile;
+#pragma unroll
+        for (int k = 0; k < K; ++k) wp[G * k + g] = a[k];
+    }
+    if (P) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) P[r][G * k + g] = a[k];
     }
 }
 
@@ -575,12 +562,14 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
     int t = __builtin_amdgcn_readfirstlane(s_task);
     if (t == 0) {
         // ---- the walker ----
-        // Per step j: wave 0 factors (j, j) and publishes its columns as they are finished;
-        // wave 3 solves (j+1, j) against them a column or two behind; waves 1 and 2 (rows 0-15
-        // and 16-31) first prepare the sub-diagonal tile (j+1, j) for wave 3 and then the next
-        // diagonal partial sum (in the other buffer). The walker is the critical path and
-        // shares its CU with the concurrent per-point kernels: its waves take issue priority on
-        // their SIMDs.
+        // Per step j: all waves add the k = j-1 term to the diagonal tile; wave 0 factors it
+        // and publishes its columns four at a time as they are finished; waves 1 and 2 (rows
+        // 0-15 and 16-31) prepare the sub-diagonal tile (j+1, j); then waves 2 and 3 solve it
+        // against the published columns, four lanes per row, behind the factor, while wave 1
+        // forms the next diagonal tile up to its k = j term (in the other buffer); wave 3
+        // publishes the previous step's sub-diagonal tile meanwhile. The walker is the critical
+        // path and shares its CU with the concurrent per-point kernels: its waves take issue
+        // priority on their SIMDs.
         __builtin_amdgcn_s_setprio(3);
         const int w = tid >> 6, lane = tid & 63;
         T (*cur)[kTile + 1] = sA;
@@ -626,6 +615,12 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
                     for (int b = 0; b < 2; ++b) cur[2 * ra + a][2 * cb + b] = acc[a][b];
                 __syncthreads();
+            }
+            if (w == 3 && j >= 1) {
+                // the previous step's sub-diagonal tile (j, j-1), stored by waves 2 and 3 before
+                // the step's barrier: published here, off the step's critical path
+                __hip_atomic_store(&flags[j * nt + j - 1], 1, __ATOMIC_RELEASE,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             }
             if (w == 0) {
                 walk_factor_t<T, true>(A, n, j, cur, sLt, sInv, dinv, sCol, tid, info, &s_prog,
@@ -681,20 +676,59 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
                 for (int a = 0; a < 4; ++a)
 #pragma unroll
                     for (int b = 0; b < 2; ++b) sC[row0 + a][col0 + b] = nx[a][b];
-                // sC (and the reads of sP above) before wave 3 starts: it overwrites sP
+                // sC (and the reads of sP above) before the solve starts: it overwrites sP
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
                 if (lane == 0) atomicAdd(&s_subready, 1);
-                // next diagonal partial sum into nxt
-                if (lane == 0 && j + 1 >= 2) df_wait(&pdf[j + 1], info);
-                T v[8];
-                walk_load16(v, A, n, j + 1, j + 1, R, lane);
+                if (w == 1) {
+                    // next diagonal tile (j+1, j+1) into nxt: the helpers' partial sum over
+                    // k < j-1, then the k = j-1 term from (j+1, j-1) (in sBw); lane (rb, cb)
+                    // holds rows 4rb .. 4rb+3, columns 4cb .. 4cb+3, every entry's chain in
+                    // increasing p
+                    if (lane == 0 && j + 1 >= 2) df_wait(&pdf[j + 1], info);
+                    const int rb4 = 4 * (lane >> 3), cb4 = 4 * (lane & 7);
+                    const int t0 = (j + 1) * kTile;
+                    T dg[4][4];
 #pragma unroll
-                for (int q = 0; q < 8; ++q) nxt[R + (lane >> 5) + 2 * q][lane & 31] = v[q];
+                    for (int a = 0; a < 4; ++a)
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            const int gr = t0 + rb4 + a, gc = t0 + cb4 + b;
+                            dg[a][b] = (gr < n && gc < n) ? A[(int64_t)gr * n + gc]
+                                                          : (gr == gc ? T(1) : T(0));
+                        }
+                    if (j >= 1) {
+                        lds_wait_ge(&s_subready, 2 * (j + 1), info);  // rows 16-31 from wave 2
+#pragma unroll 1
+                        for (int p0 = 0; p0 < kTile; p0 += V) {
+                            Q rv[4], cq[4];
+#pragma unroll
+                            for (int a = 0; a < 4; ++a) rv[a] = *reinterpret_cast<const Q*>(&sBw[rb4 + a][p0]);
+#pragma unroll
+                            for (int b = 0; b < 4; ++b) cq[b] = *reinterpret_cast<const Q*>(&sBw[cb4 + b][p0]);
+#pragma unroll
+                            for (int u = 0; u < V; ++u)
+#pragma unroll
+                                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                                    for (int b = 0; b < 4; ++b)
+                                        dg[a][b] = num<T>::fma(-rv[a].e[u], cq[b].e[u], dg[a][b]);
+                        }
+                    }
+#pragma unroll
+                    for (int a = 0; a < 4; ++a)
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) nxt[rb4 + a][cb4 + b] = dg[a][b];
+                } else {
+                    // rows 0-15 of the solve
+                    lds_wait_ge(&s_subready, 2 * (j + 1), info);
+                    walk_solve_grp<T, 4, true>(A, n, j + 1, j, sC, sLt, sP, tid - 128, &s_prog,
+                                               j * kTile, info);
+                }
             } else if (sub && w == 3) {
+                // rows 16-31 of the solve (wave 3 publishes the tile in the next step)
                 lds_wait_ge(&s_subready, 2 * (j + 1), info);
-                walk_solve_stream(A, n, j + 1, j, sC, sLt, sP, lane, &s_prog, j * kTile, info);
-                __hip_atomic_store(&flags[(j + 1) * nt + j], 1, __ATOMIC_RELEASE,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+                walk_solve_grp<T, 4, true>(A, n, j + 1, j, sC, sLt, sP, tid - 128, &s_prog,
+                                           j * kTile, info);
             }
             __syncthreads();
             T (*tmp)[kTile + 1] = cur;
@@ -718,28 +752,32 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
             walk_accumulate(acc, A, n, nt, i, g, 0, g, flags, info, sA, sB, tid, r0, c);
             if (tid == 0) df_wait(&flags[g * nt + g], info);
             __syncthreads();
+            // L[g][g] transposed into sLt in the order of walk_perm<8>
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int r = r0 + 8 * q;
                 sA[r][c] = acc[q];
-                sB[r][c] = (g * kTile + r < n && c <= r) ? A[(int64_t)(g * kTile + r) * n + g * kTile + c] : T(0);
+                sLt[c][walk_perm<8>(r)] =
+                    (g * kTile + r < n && c <= r) ? A[(int64_t)(g * kTile + r) * n + g * kTile + c] : T(0);
             }
-            if (kRsqFactor<T> && tid < kTile)
-                sInv[tid] = g * kTile + tid < n ? dinv[g * kTile + tid] : T(1);
             __syncthreads();
-            if (tid < 64) walk_solve(A, n, i, g, sA, sB, sInv, (T(*)[kTile + 1])nullptr, tid);
+            walk_solve_grp<T, 8, false>(A, n, i, g, sA, sLt, (T(*)[kLtPitch])nullptr, tid, nullptr, 0,
+                                        info);
             __syncthreads();
             if (tid == 0) {
                 __hip_atomic_store(&flags[i * nt + g], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
                 s_task = atomicAdd(ticket, 1);
             }
         } else {
-            // partial sum over k < g+1 of the walker's tile (d, d) or (d+1, d), d = g+2
+            // partial sums for the walker, d = g+2: of its tile (d, d) over k < g (the walker
+            // adds k = g from the tile (d, g) it holds for its sub-diagonal tile), of (d+1, d)
+            // over k < g+1
             const int d = g + 2;
             const bool diag = rem == nreg;
             const int i = diag ? d : d + 1;
             walk_load(acc, A, n, i, d, r0, c);
-            walk_accumulate(acc, A, n, nt, i, d, 0, d - 1, flags, info, sA, sB, tid, r0, c);
+            walk_accumulate(acc, A, n, nt, i, d, 0, diag ? g : g + 1, flags, info, sA, sB, tid, r0,
+                            c);
             // (the diagonal tile keeps its upper triangle, which no one reads)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -784,7 +822,6 @@ __global__ void __launch_bounds__(kDfThreads) k_panel_step(T* __restrict__ A, in
                                                            int* __restrict__ info) {
     __shared__ T sA[kTile][kTile + 1];
     __shared__ T sB[kTile][kTile + 1];
-    __shared__ T sC[kTile][kTile + 1];
     __shared__ __align__(16) T sLt[kTile][kLtPitch];
     __shared__ T sInv[kTile];
     __shared__ __align__(16) T sCol[2][kTile];
@@ -819,15 +856,16 @@ __global__ void __launch_bounds__(kDfThreads) k_panel_step(T* __restrict__ A, in
     }
     if (tid == 0) df_wait(flag, info);
     __syncthreads();
-    // L[s][s] transposed, zero above the diagonal (rows past n: the identity's)
+    // L[s][s] transposed in the order of walk_perm<8>, zero above the diagonal (rows past n: the
+    // identity's)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int r = r0 + 8 * q;
         T v = c <= r ? (s0r + r < n ? A[(int64_t)(s0r + r) * n + s0r + c] : T(r == c ? 1 : 0)) : T(0);
-        sLt[c][r] = v;
+        sLt[c][walk_perm<8>(r)] = v;
     }
     __syncthreads();
-    if (tid < 64) walk_solve_t(A, n, i, s, sA, sLt, sInv, sC, tid);
+    walk_solve_grp<T, 8, false>(A, n, i, s, sA, sLt, (T(*)[kLtPitch])nullptr, tid, nullptr, 0, info);
 }
 
 // A[r][c] = fma(-A[r][k], A[c][k], A[r][c]) for k = k0, ..., k0 + kd - 1 over the lower blocks of

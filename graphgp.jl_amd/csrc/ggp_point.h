@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace ggp {
 
 template <typename T> struct num;
@@ -47,6 +49,17 @@ template <typename T>
 __device__ inline T div_rcp(T t, T d, T y) {
     const T q0 = t * y;
     return num<T>::fma(num<T>::fma(-q0, d, t), y, q0);
+}
+
+// f(integral_constant<int, I>) for I = B .. E-1, each call its own inlined copy (a loop whose
+// body is too large for the unroller's budget would otherwise keep a run-time index into the
+// lanes' register arrays and send them to scratch memory).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
 }
 
 // ---- cross-lane moves (wave-uniform lane index; call from wave-uniform control flow) --------

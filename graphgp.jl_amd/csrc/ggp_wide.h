@@ -33,17 +33,6 @@ constexpr int kGrp = 32;                     // lanes per point = rows of the pa
 constexpr int kGrpPt = kGrp - 1;             // the point's row
 constexpr int kWideWaves = kWideBlock / 64;  // wavefronts per workgroup
 
-// f(integral_constant<int, I>) for I = B .. E-1, each call its own inlined copy (a loop whose
-// body is too large for the unroller's budget would otherwise keep a run-time index into the
-// lanes' register arrays and send them to scratch memory).
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (B < E) {
-        f(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(f);
-    }
-}
-
 // 16 bytes of T (one LDS vector access).
 template <typename T>
 struct alignas(16) Q16 {
