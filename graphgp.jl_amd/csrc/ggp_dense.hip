@@ -323,11 +323,13 @@ __host__ __device__ inline int dense_sync_flag_ints(int nt) { return (nt * nt + 
 // above the diagonal). Right-looking by columns on one wavefront: lane 32h + r holds row r,
 // columns 16h .. 16h+15. At step p the pivot comes from its lane by readlane; the lanes holding
 // column p scale it and publish it to LDS (col, rows <= p as zero), and every lane reads its 16
-// column values back with broadcast reads and updates all 16 of its entries: entry (r, c) takes
-// fma(-L[r][p], L[c][p], .) when p < c, and fma(-L[r][p], 0, .) (no change) otherwise, so each
-// entry keeps the unblocked left-looking chain in its order. Entries above the diagonal are
-// scratch (updated, never stored).
-// L[p][p] = sqrt(pivot) and the column divided by it (the oracle's bits). With kRsqFactor (off):
+// column values back with broadcast reads and updates its entries: entry (r, c) takes
+// fma(-L[r][p], L[c][p], .) when p < c, so each entry keeps the unblocked left-looking chain in
+// its order; a finished entry (c <= p) takes fma(-L[r][p], 0, .), no change but for the sign of
+// a zero, until p = 15 and nothing after (both halves skip columns that are finished in both).
+// Entries above the diagonal are scratch (updated, never stored).
+// L[p][p] = sqrt(pivot) (f32: sqrt_rn_any_f32, the same bits) and the column divided by it (the
+// oracle's bits). With kRsqFactor (off):
 // one reciprocal square root per column (v_rsq_f32, within 1 ulp), L[p][p] = pivot * rsq and
 // the column multiplied by rsq, which takes the square root and the division off the
 // column-to-column chain; rsq then goes to inv (LDS) and dinv (global, for the helpers' solves).
@@ -359,7 +361,8 @@ __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[
             l = a[up] * rs;
             myinv = (mine && r == p) ? rs : myinv;
         } else {
-            d = num<T>::sqrt(piv);
+            if constexpr (std::is_same<T, float>::value) d = sqrt_rn_any_f32(piv);
+            else d = num<T>::sqrt(piv);
             l = a[up] / d;
         }
         a[up] = mine ? (r == p ? d : l) : a[up];
@@ -375,8 +378,11 @@ __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[
         T cv[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) cv[u] = cp[16 * h + u];
+        // columns <= p are finished: past p = 15 both halves skip them (below, every lane's
+        // column u of half 0 is finished, and cv is zero there)
 #pragma unroll
-        for (int u = 0; u < 16; ++u) a[u] = num<T>::fma(-own, cv[u], a[u]);
+        for (int u = 0; u < 16; ++u)
+            if (p < 16 || u > p - 16) a[u] = num<T>::fma(-own, cv[u], a[u]);
     }
     const bool diag_lane = h == (r >> 4);  // holds L[r][r] (and its reciprocal)
     if (live) {

@@ -212,7 +212,8 @@ template <typename T>
 void launch_points_out(T* out, const double* dp, const double* dpd, int64_t N, int D,
                        int64_t n_dense, const int32_t* map, hipStream_t st);
 
-// Self-check of the lattice square root (sqrt_rn_f32) over bit patterns [b0, b0 + count).
+// Self-check of the f32 square roots (sqrt_rn_f32 in its range, sqrt_rn_any_f32 everywhere) over
+// bit patterns [b0, b0 + count).
 void launch_sqrt_check(uint32_t b0, uint32_t count, unsigned long long* bad, hipStream_t st);
 // Self-check of div_rcp against the IEEE division (f32: divisor bit patterns [b0, b0 + count);
 // f64: count random divisors), `per` numerators per divisor.

@@ -320,15 +320,20 @@ void launch_div_check(int f64, uint64_t b0, uint64_t count, uint32_t per, uint64
     hipLaunchKernelGGL(k_div_check, dim3(4096), dim3(256), 0, st, f64, b0, count, per, seed, bad);
 }
 
-// Self-check of sqrt_rn_f32 against the correctly rounded sqrtf over `count` consecutive bit
-// patterns from b0; *bad receives the number of differing results.
+// Self-check of the square roots against the correctly rounded sqrtf over `count` consecutive
+// bit patterns from b0: sqrt_rn_any_f32 everywhere (NaN results match any NaN), sqrt_rn_f32 on 0
+// and [1e-30, 2^64]; *bad receives the number of differing results.
 __global__ void __launch_bounds__(256) k_sqrt_check(uint32_t b0, uint32_t count,
                                                     unsigned long long* __restrict__ bad) {
     const uint32_t stride = gridDim.x * blockDim.x;
     unsigned long long nbad = 0;
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
         const float x = __uint_as_float(b0 + i);
-        nbad += __float_as_uint(sqrt_rn_f32(x)) != __float_as_uint(__builtin_sqrtf(x));
+        const float ref = __builtin_sqrtf(x);
+        const float any = sqrt_rn_any_f32(x);
+        nbad += ref != ref ? any == any : __float_as_uint(any) != __float_as_uint(ref);
+        if (x == 0.f || (x >= 1e-30f && x <= 0x1p64f))
+            nbad += __float_as_uint(sqrt_rn_f32(x)) != __float_as_uint(ref);
     }
     if (nbad) atomicAdd(bad, nbad);
 }

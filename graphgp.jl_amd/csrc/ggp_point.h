@@ -228,6 +228,17 @@ __device__ inline float sqrt_rn_f32(float x) {
     const float y = rdn <= 0.f ? sdn : s;
     return rup > 0.f ? sup : y;
 }
+// Correctly rounded sqrtf(x) for every float x, from sqrt_rn_f32 by exact scaling: with e the
+// exponent field of x and m = floor((e - 127) / 2), x 4^-m lies in [2^-23, 4) (subnormals
+// included), inside sqrt_rn_f32's range, and sqrt(x) = sqrt(x 4^-m) 2^m with both scalings exact
+// (the root of a positive float is normal); zeros, infinities and NaN pass through. For a
+// wave-uniform x, m is scalar arithmetic and the sequence is shorter than the general one.
+// Checked against sqrtf bit for bit over every float (selftest_sqrt; NaN results compared as
+// NaN).
+__device__ inline float sqrt_rn_any_f32(float x) {
+    const int m = ((int)((__float_as_uint(x) >> 23) & 255u) - 127) >> 1;
+    return __builtin_amdgcn_ldexpf(sqrt_rn_f32(__builtin_amdgcn_ldexpf(x, -2 * m)), m);
+}
 template <typename T> __device__ inline T sqrt_lattice(T x) { return num<T>::sqrt(x); }
 template <> __device__ inline float sqrt_lattice<float>(float x) { return sqrt_rn_f32(x); }
 

@@ -243,10 +243,12 @@ int ggp_build_graph_device(const double* points, int64_t N, int32_t D, int64_t n
 int ggp_kernel_timers(ggp_graph* h, int32_t enable);
 int ggp_kernel_timer_read(const ggp_graph* h, const char* name, double* total_ms, int64_t* count);
 
-/* No counterpart in the reference. Self-check of the f32 square root the per-point kernels use
- * for pair radii (a correctly rounded sqrt without range scaling): compares it bit for bit with
- * sqrtf on the current device over the `count` float bit patterns starting at `first_bits` and
- * stores the number of differences. Synchronous. */
+/* No counterpart in the reference. Self-check of the f32 square roots: the one the per-point
+ * kernels use for pair radii (a correctly rounded sqrt without range scaling, on 0 and
+ * [1e-30, 2^64]) and the range-reduced one of the dense factor's pivots (every float; NaN
+ * results compared as NaN). Compares them bit for bit with sqrtf on the current device over the
+ * `count` float bit patterns starting at `first_bits` and stores the number of differences.
+ * Synchronous. */
 int ggp_selftest_sqrt_f32(uint32_t first_bits, uint32_t count, uint64_t* mismatches);
 
 /* No counterpart in the reference. Self-check of the division the per-point Cholesky and

@@ -42,3 +42,14 @@ def test_cholesky_division_matches_ieee_f64(gpu):
     bad = C.c_uint64(0)
     nat.call("ggp_selftest_div", 1, 0, 1 << 26, 8, 7, C.byref(bad))
     assert bad.value == 0
+
+
+@pytest.mark.parametrize("part", range(4))
+def test_pivot_sqrt_is_correctly_rounded_everywhere(gpu, part):
+    """The dense factor's f32 pivots go through the range-reduced square root; over every float
+    bit pattern (a quarter per case: positive and negative, zero, subnormal, infinite, NaN) it
+    must equal sqrtf bit for bit (NaN for NaN)."""
+    from graphgp_hip import _native as nat
+    bad = C.c_uint64(0)
+    nat.call("ggp_selftest_sqrt_f32", part << 30, 1 << 30, C.byref(bad))
+    assert bad.value == 0
