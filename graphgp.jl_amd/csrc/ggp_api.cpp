@@ -1093,7 +1093,7 @@ int ggp_selftest_div(int32_t dtype, uint64_t first, uint64_t count, uint32_t per
     unsigned long long* d = nullptr;
     HC(hipMalloc((void**)&d, sizeof(*d)));
     hipError_t e = hipMemset(d, 0, sizeof(*d));
-    if (e == hipSuccess && count && per_divisor) {
+    if (e == hipSuccess && count && (per_divisor || dtype == GGP_F32)) {  // f32: the reciprocal too
         ggp::launch_div_check(dtype == GGP_F64, first, count, per_divisor, seed, d, nullptr);
         e = hipGetLastError();
     }

@@ -425,9 +425,9 @@ __device__ __forceinline__ int lds_wait_ge(const int* v, int target, int* info) 
 // group by a DPP broadcast (quad_perm for G <= 4; for G = 8, row_newbcast into each half of a
 // 16-lane row), after which every later column of the row takes fma(-x, L[c][p], .): each
 // entry receives the row-by-row substitution's terms in its order, then its division, which is
-// div_rcp with RN(1 / L[c][c]) (the IEEE quotient). L comes transposed and permuted:
-// Lp[p][walk_perm<G>(c)] = L[c][p], zero for c < p, so a lane's values of column p are
-// 16-byte aligned and contiguous.
+// div_rcp with RN(1 / L[c][c]) from rcp_rn (together the IEEE quotient). L comes transposed and
+// permuted: Lp[p][walk_perm<G>(c)] = L[c][p], zero for c < p, so a lane's values of column p
+// are 16-byte aligned and contiguous.
 template <int G, int O>
 constexpr int walk_qsel() {
     int s = 0;
@@ -483,7 +483,7 @@ __device__ __forceinline__ void walk_solve_grp(T* A, int n, int i, int j, const 
 #pragma unroll
         for (int k = 0; k < K; ++k) dv[k] = Lp[G * k + g][g * K + k];
 #pragma unroll
-        for (int k = 0; k < K; ++k) yv[k] = T(1) / dv[k];
+        for (int k = 0; k < K; ++k) yv[k] = rcp_rn(dv[k]);
     }
     T piv = a[0];  // on lane p mod G: column p, all earlier terms in
     int avail = 0;  // STREAM: columns of L seen to be out (a wait only when past them)
@@ -493,7 +493,7 @@ __device__ __forceinline__ void walk_solve_grp(T* A, int n, int i, int j, const 
         if constexpr (STREAM && p % 4 == 0) {
             if (avail < p + 4) avail = lds_wait_ge(prog, pbase + p + 4, info) - pbase;
             dv[ko] = Lp[p + g][g * K + ko];
-            yv[ko] = T(1) / dv[ko];
+            yv[ko] = rcp_rn(dv[ko]);
         }
         const T x = div_rcp(piv, dv[ko], yv[ko]);
         const T xb = walk_gbcast<G, go>(x);

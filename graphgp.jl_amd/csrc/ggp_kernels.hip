@@ -292,6 +292,11 @@ __global__ void __launch_bounds__(256) k_div_check(int f64, uint64_t b0, uint64_
         if (!f64) {
             const float d = __uint_as_float((uint32_t)(b0 + i));
             const float y = 1.0f / d;
+            // the reciprocal the kernels use (equal to 1/d on [2^-126, 2^126) and at 0, inf, NaN)
+            const float yr = ggp::rcp_rn(d);
+            const bool in = __builtin_fabsf(d) >= 0x1p-126f && __builtin_fabsf(d) < 0x1p126f;
+            if (in || d == 0.f || __builtin_isinf(d)) nbad += __float_as_uint(yr) != __float_as_uint(y);
+            else if (d != d) nbad += yr == yr;
             for (uint32_t u = 0; u < per; ++u) {
                 const uint64_t h = mix64(seed ^ (i * 0x100000001b3ull + u));
                 const uint32_t e = 27u + (uint32_t)((h >> 32) % 201u);  // 2^-100 .. 2^100

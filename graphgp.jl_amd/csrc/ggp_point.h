@@ -38,7 +38,7 @@ template <> struct num<double> {
     __device__ static inline bits_t bits(double a) { return (bits_t)__double_as_longlong(a); }
 };
 
-// t / d rounded once, given y = RN(1/d) (one IEEE division per divisor): q0 = t*y lies within
+// t / d rounded once, given y = RN(1/d) (rcp_rn, one per divisor): q0 = t*y lies within
 // an ulp of t/d, the remainder t - d*q0 is exact in one fma, and q0 + (t - d*q0)*y rounded once
 // is the correctly rounded quotient (Markstein's correction step, as in the IA-64 division
 // sequences). It equals the IEEE division whenever the remainder is representable and nothing
@@ -60,6 +60,22 @@ __device__ __forceinline__ void static_for(F&& f) {
         f(std::integral_constant<int, B>{});
         static_for<B + 1, E>(f);
     }
+}
+
+// RN(1/d), the IEEE quotient: f32 through v_rcp_f32 (within 1 ulp) and one Newton step
+// r + r(1 - d r) with the residual exact in one fma, which equals 1/d for every d in
+// [2^-126, 2^126) (ggp_selftest_div compares the two for each divisor it takes); zeros,
+// infinities and NaN (whose residual is NaN) keep v_rcp_f32's result, which is 1/d there.
+// Subnormal and larger d never reach it (it divides by square roots of positive floats).
+template <typename T>
+__device__ inline T rcp_rn(T d) {
+    return T(1) / d;
+}
+template <>
+__device__ inline float rcp_rn<float>(float d) {
+    const float r = __builtin_amdgcn_rcpf(d);
+    const float e = __builtin_fmaf(-d, r, 1.0f);
+    return e == e ? __builtin_fmaf(e, r, r) : r;
 }
 
 // ---- cross-lane moves (wave-uniform lane index; call from wave-uniform control flow) --------
@@ -489,7 +505,7 @@ struct Block {
             const bool ok = s > pivmin;  // false for NaN, as in the reference
             const T d = ok ? num<T>::sqrt(s) : dmin;
             A[tri(j, j)] = d;
-            if (j < K) rd[j] = T(1) / d;
+            if (j < K) rd[j] = rcp_rn(d);
 #pragma unroll
             for (int i = j + 1; i < N; ++i) {
                 T t = A[tri(i, j)];

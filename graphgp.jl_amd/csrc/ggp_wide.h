@@ -152,7 +152,7 @@ __device__ __forceinline__ T grp_cholesky(T (&a)[kGrp], T* xv, T* rd, int K, int
             const T s = gbcast(a[j], j, hi);
             const bool ok = s > pivmin;  // false for NaN, as in the reference
             const T d = ok ? num<T>::sqrt(s) : dmin;
-            const T y = T(1) / d;
+            const T y = rcp_rn(d);
             if (r == 0) rd[j] = y;
             const T q = div_rcp(a[j], d, y);
             a[j] = r == j ? d : (r > j ? (ok ? q : T(0)) : a[j]);

@@ -251,13 +251,14 @@ int ggp_kernel_timer_read(const ggp_graph* h, const char* name, double* total_ms
  * Synchronous. */
 int ggp_selftest_sqrt_f32(uint32_t first_bits, uint32_t count, uint64_t* mismatches);
 
-/* No counterpart in the reference. Self-check of the division the per-point Cholesky and
- * mean_vec use: t / d from one reciprocal per divisor with a one-fma remainder correction,
- * compared bit for bit with the IEEE division on the current device. GGP_F32: every divisor
- * bit pattern in [first, first + count); GGP_F64: `count` random divisors in [2^-60, 2^60)
- * drawn from `seed`. Each divisor gets per_divisor numerators (zero, then random ones over
- * 2^-100 .. 2^100 in f32 or 2^-900 .. 2^900 in f64). Stores the number of differences.
- * Synchronous. */
+/* No counterpart in the reference. Self-check of the division the per-point Cholesky,
+ * mean_vec and the dense tile solves use: t / d from one reciprocal per divisor with a one-fma
+ * remainder correction, compared bit for bit with the IEEE division on the current device.
+ * GGP_F32: every divisor bit pattern in [first, first + count), whose reciprocal (v_rcp_f32 and
+ * one Newton step) is also compared with 1/d (on [2^-126, 2^126), zeros and infinities; NaN
+ * for NaN); GGP_F64: `count` random divisors in [2^-60, 2^60) drawn from `seed`. Each divisor
+ * gets per_divisor numerators (zero, then random ones over 2^-100 .. 2^100 in f32 or
+ * 2^-900 .. 2^900 in f64). Stores the number of differences. Synchronous. */
 int ggp_selftest_div(int32_t dtype, uint64_t first, uint64_t count, uint32_t per_divisor,
                      uint64_t seed, uint64_t* mismatches);
 

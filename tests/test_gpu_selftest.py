@@ -53,3 +53,22 @@ def test_pivot_sqrt_is_correctly_rounded_everywhere(gpu, part):
     bad = C.c_uint64(0)
     nat.call("ggp_selftest_sqrt_f32", part << 30, 1 << 30, C.byref(bad))
     assert bad.value == 0
+
+
+@pytest.mark.parametrize("lo,hi", [(2.0 ** -126, 2.0 ** 0), (2.0 ** 0, 2.0 ** 126)])
+def test_reciprocal_matches_ieee_f32(gpu, lo, hi):
+    """The kernels' f32 reciprocal (v_rcp_f32 and one Newton step) against 1/d for every divisor
+    bit pattern of the normal range (no numerators: the reciprocal alone)."""
+    from graphgp_hip import _native as nat
+    b0, b1 = _bits(lo), _bits(hi)
+    bad = C.c_uint64(0)
+    nat.call("ggp_selftest_div", 0, b0, b1 - b0, 0, 1, C.byref(bad))
+    assert bad.value == 0
+
+
+@pytest.mark.parametrize("x", [0.0, -0.0, float("inf"), float("-inf"), float("nan")])
+def test_reciprocal_special_values_f32(gpu, x):
+    from graphgp_hip import _native as nat
+    bad = C.c_uint64(0)
+    nat.call("ggp_selftest_div", 0, _bits(x), 1, 0, 1, C.byref(bad))
+    assert bad.value == 0
