@@ -10,6 +10,7 @@
 // the same derivative evaluated in a parallel order.
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "ggp_internal.h"
@@ -25,13 +26,20 @@ __global__ void k_dense_assemble(T* __restrict__ A, const uint32_t* __restrict__
                                  T scale, const TabEnt<T>* __restrict__ tab,
                                  const uint16_t* __restrict__ acc, const TabParams<T>* __restrict__ Pp, T diag_add,
                                  AnisoArgs<T> an, int* __restrict__ z0, int n_z0,
-                                 int* __restrict__ z1, int n_z1) {
-    // Side job of the first workgroup: zero the factor's status and task flags (z0, z1), so the
-    // Cholesky launch follows this one directly.
+                                 int* __restrict__ z1, int n_z1, T* __restrict__ mb,
+                                 int64_t n_mb, T mbv) {
+    // Side jobs, so the Cholesky launch follows this one directly: the first workgroup zeroes
+    // the factor's status and task flags (z0, z1); all of them set its mailboxes (mb) to the
+    // pending marker mbv.
     if (blockIdx.x == 0 && blockIdx.y == 0) {
         const int t = threadIdx.y * 16 + threadIdx.x;
         for (int q = t; q < n_z0; q += 256) z0[q] = 0;
         for (int q = t; q < n_z1; q += 256) z1[q] = 0;
+    }
+    if (n_mb) {
+        const int64_t nb = (int64_t)gridDim.x * gridDim.y;
+        const int64_t b = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+        for (int64_t q = b * 256 + threadIdx.y * 16 + threadIdx.x; q < n_mb; q += nb * 256) mb[q] = mbv;
     }
     if (blockIdx.x > blockIdx.y) return;  // the whole block lies above the diagonal
     extern __shared__ __align__(16) unsigned char smem[];
@@ -318,6 +326,15 @@ __host__ __device__ constexpr int walk_perm(int c) {
 // sync = [ticket, tile flags[nt*nt], diagonal-partial flags[nt], sub-diagonal-partial flags[nt],
 // (padding to 8 bytes), reciprocal diagonal[nt*kTile] (f32 walker)]: ints before the last part.
 __host__ __device__ inline int dense_sync_flag_ints(int nt) { return (nt * nt + 2 * nt + 2) & ~1; }
+// After the reciprocal diagonal (2 nt kTile ints): the walker's two mailboxes, each nt tiles of
+// kTile x kTile values of the element type, published value by value (sweep_publish): L[g][g]
+// for the helpers' solves, and the helpers' L[g+2][g] for the walker's sub-diagonal term. They
+// hold the pending marker before a launch.
+template <typename T>
+__host__ __device__ inline T* dense_mbox(int* sync, int nt) {
+    return reinterpret_cast<T*>(sync + dense_sync_flag_ints(nt) + 2 * nt * kTile);
+}
+__host__ __device__ inline int64_t dense_mbox_values(int nt) { return (int64_t)2 * nt * kTile * kTile; }
 
 // Walker factor of the tile in sA into global tile (j, j) and, transposed, into Lt (LDS; zero
 // above the diagonal). Right-looking by columns on one wavefront: lane 32h + r holds row r,
@@ -339,7 +356,8 @@ __host__ __device__ inline int dense_sync_flag_ints(int nt) { return (nt * nt + 
 template <typename T, bool STREAM = false>
 __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[kTile + 1],
                                      T (*Lt)[kLtPitch], T* inv, T* dinv, T (*col)[kTile],
-                                     int tid, int* info, int* prog = nullptr, int pbase = 0) {
+                                     int tid, int* info, int* prog = nullptr, int pbase = 0,
+                                     T* mbox = nullptr) {
     constexpr bool kRsq = kRsqFactor<T>;
     const int r = tid & (kTile - 1), h = tid >> 5;
     const bool live = j * kTile + r < n;
@@ -391,6 +409,10 @@ __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[
         for (int u = 0; u < 16; ++u)
             if (16 * h + u <= r) wp[u] = a[u];
         if (kRsq && diag_lane) dinv[j * kTile + r] = myinv;
+    }
+    if (mbox) {  // the whole tile, row-major, value by value
+#pragma unroll
+        for (int u = 0; u < 16; ++u) sweep_publish(&mbox[r * kTile + 16 * h + u], a[u]);
     }
     if (kRsq && diag_lane) inv[r] = myinv;
     if (!STREAM) {
@@ -460,15 +482,17 @@ __device__ __forceinline__ double walk_gbcast(double x) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
-// Solves X L^T = B for the 32 x 32 tile B in sX into global tile (i, j) (rows below n) and, if P
-// is given, into P. Threads gt = 0 .. 32 G - 1 take part: lane (gt & 63) of wavefront gt >> 6
-// holds row (gt >> 6) * (64 / G) + (gt & 63) / G. STREAM (G = 4): the columns of L arrive four
-// at a time from walk_factor_t<T, true> on another wavefront; before column p = 4b a wavefront
-// that has not yet seen *prog >= pbase + 4b + 4 waits for it.
+// Solves X L^T = B for the 32 x 32 tile B in sX into global tile (i, j) (rows below n), if P is
+// given into P, and if mbox is given into that mailbox tile (sweep_publish). Threads
+// gt = 0 .. 32 G - 1 take part: lane (gt & 63) of wavefront gt >> 6 holds row
+// (gt >> 6) * (64 / G) + (gt & 63) / G. STREAM (G = 4): the columns of L arrive four at a time
+// from walk_factor_t<T, true> on another wavefront; before column p = 4b a wavefront that has
+// not yet seen *prog >= pbase + 4b + 4 waits for it.
 template <typename T, int G, bool STREAM>
 __device__ __forceinline__ void walk_solve_grp(T* A, int n, int i, int j, const T (*sX)[kTile + 1],
                                                const T (*Lp)[kLtPitch], T (*P)[kLtPitch], int gt,
-                                               const int* prog, int pbase, int* info) {
+                                               const int* prog, int pbase, int* info,
+                                               T* mbox = nullptr) {
     static_assert(!kRsqFactor<T>, "the division by L[p][p] is the IEEE quotient");
     static_assert(!STREAM || G == 4, "a streamed batch of four columns is one k");
     constexpr int K = kTile / G;
@@ -522,6 +546,10 @@ __device__ __forceinline__ void walk_solve_grp(T* A, int n, int i, int j, const 
 #pragma unroll
         for (int k = 0; k < K; ++k) P[r][G * k + g] = a[k];
     }
+    if (mbox) {  // the tile, row-major, value by value
+#pragma unroll
+        for (int k = 0; k < K; ++k) sweep_publish(&mbox[r * kTile + G * k + g], a[k]);
+    }
 }
 
 // Rows [R, R+16) of tile (i, j) for a 64-lane wavefront: lane l holds (R + (l >> 5) + 2q, l & 31).
@@ -557,6 +585,8 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
     int* pdf = flags + nt * nt;
     int* psf = pdf + nt;
     T* dinv = reinterpret_cast<T*>(sync + dense_sync_flag_ints(nt));
+    T* mb_diag = dense_mbox<T>(sync, nt);                       // L[g][g]
+    T* mb_sub = mb_diag + (int64_t)nt * kTile * kTile;         // L[g+2][g]
     const int tid = threadIdx.x;
     const int c = tid & (kTile - 1), r0 = tid >> 5;
     if (tid == 0) {
@@ -629,9 +659,9 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
                                    __HIP_MEMORY_SCOPE_AGENT);
             }
             if (w == 0) {
+                // L[j][j] goes to the helpers through its mailbox tile (no flag, no release)
                 walk_factor_t<T, true>(A, n, j, cur, sLt, sInv, dinv, sCol, tid, info, &s_prog,
-                                       j * kTile);
-                __hip_atomic_store(&flags[j * nt + j], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                                       j * kTile, mb_diag + (int64_t)j * kTile * kTile);
             } else if (sub && w <= 2) {
                 // sub-diagonal tile: partial sum over k < j-1 plus the k = j-1 term, into sC.
                 // Lane (rb, cb) of wave w holds rows R + 4rb .. R + 4rb + 3, columns 2cb, 2cb + 1;
@@ -652,10 +682,21 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
                         const int gr = (j + 1) * kTile + row0 + a;
                         nx[a][b] = gr < n ? A[(int64_t)gr * n + j * kTile + col0 + b] : T(0);
                     }
-                if (lane == 0 && j >= 1) df_wait(&flags[(j + 1) * nt + j - 1], info);
                 if (j >= 1) {
+                    // the helpers' L[j+1][j-1], read value by value from its mailbox tile
                     T lo[8];
-                    walk_load16(lo, A, n, j + 1, j - 1, R, lane);
+                    {
+                        const T* mt = mb_sub + (int64_t)(j - 1) * kTile * kTile;
+                        int64_t idx[8];
+                        bool live[8];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) {
+                            const int r = R + (lane >> 5) + 2 * q;
+                            idx[q] = r * kTile + (lane & 31);
+                            live[q] = (j + 1) * kTile + r < n;
+                        }
+                        sweep_read_all<T, 8>(lo, mt, idx, live, info, 2);
+                    }
 #pragma unroll
                     for (int q = 0; q < 8; ++q) sBw[R + (lane >> 5) + 2 * q][lane & 31] = lo[q];
                     wave_sync_lds();
@@ -756,19 +797,31 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
             const int i = g + 2 + rem;
             walk_load(acc, A, n, i, g, r0, c);
             walk_accumulate(acc, A, n, nt, i, g, 0, g, flags, info, sA, sB, tid, r0, c);
-            if (tid == 0) df_wait(&flags[g * nt + g], info);
-            __syncthreads();
-            // L[g][g] transposed into sLt in the order of walk_perm<8>
+            // L[g][g] (a full tile: g < nt-2) from its mailbox, transposed into sLt in the order
+            // of walk_perm<8>
+            {
+                T lv[4];
+                int64_t idx[4];
+                bool live[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int r = r0 + 8 * q;
-                sA[r][c] = acc[q];
-                sLt[c][walk_perm<8>(r)] =
-                    (g * kTile + r < n && c <= r) ? A[(int64_t)(g * kTile + r) * n + g * kTile + c] : T(0);
+                for (int q = 0; q < 4; ++q) {
+                    const int r = r0 + 8 * q;
+                    idx[q] = r * kTile + c;
+                    live[q] = c <= r;
+                }
+                sweep_read_all<T, 4>(lv, mb_diag + (int64_t)g * kTile * kTile, idx, live, info, 2);
+                __syncthreads();  // the previous task's reads of sA and sLt are done
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = r0 + 8 * q;
+                    sA[r][c] = acc[q];
+                    sLt[c][walk_perm<8>(r)] = lv[q];
+                }
             }
             __syncthreads();
+            // the walker reads (g+2, g) for its sub-diagonal term from the mailbox
             walk_solve_grp<T, 8, false>(A, n, i, g, sA, sLt, (T(*)[kLtPitch])nullptr, tid, nullptr, 0,
-                                        info);
+                                        info, i == g + 2 ? mb_sub + (int64_t)g * kTile * kTile : nullptr);
             __syncthreads();
             if (tid == 0) {
                 __hip_atomic_store(&flags[i * nt + g], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -961,14 +1014,28 @@ void dense_potrf_blocked(T* A, int n, int* info, int* flags, hipStream_t st) {
 
 int dense_sync_ints(int n) {
     const int nt = (n + kTile - 1) / kTile;
-    return dense_sync_flag_ints(nt) + 2 * nt * kTile;  // + the reciprocal diagonal (<= f64)
+    // + the reciprocal diagonal and the walker's two mailboxes (<= f64)
+    return dense_sync_flag_ints(nt) + 2 * nt * kTile + (int)(2 * dense_mbox_values(nt));
+}
+
+template <typename T>
+static T pending_value() {
+    T v;
+    const auto b = Pending<T>::bits;
+    static_assert(sizeof(b) == sizeof(T), "marker width");
+    std::memcpy(&v, &b, sizeof(T));
+    return v;
 }
 
 template <typename T>
 void dense_potrf(T* A, int n, int* info, int* sync, int max_wg, hipStream_t st, bool zeroed) {
     if (n <= 0) return;
     const int nt = (n + kTile - 1) / kTile;
-    if (!zeroed) launch_fill<int>(sync, 0, dense_sync_flag_ints(nt), st);
+    if (!zeroed) {
+        launch_fill<int>(sync, 0, dense_sync_flag_ints(nt), st);
+        if (!dense_blocked(n))
+            launch_fill<T>(dense_mbox<T>(sync, nt), pending_value<T>(), dense_mbox_values(nt), st);
+    }
     if (dense_blocked(n)) {
         dense_potrf_blocked(A, n, info, sync + 1, st);  // flags: one per tile column
         return;
@@ -1201,15 +1268,20 @@ void dense_logdiag(const T* L, int n, double* out, hipStream_t st) {
 template <typename T>
 void dense_assemble(const Graph& g, const Table<T>& tb, T* A, T diag_add, hipStream_t st,
                     int* zero_info, int* zero_sync) {
-    const int nz1 = zero_sync ? dense_sync_flag_ints(cdiv((int)g.n0, kTile)) : 0;
+    const int nt0 = (int)cdiv((int)g.n0, kTile);
+    const int nz1 = zero_sync ? dense_sync_flag_ints(nt0) : 0;
+    // the walker's mailboxes (the blocked factor has none)
+    T* mb = zero_sync && !dense_blocked((int)g.n0) ? dense_mbox<T>(zero_sync, nt0) : nullptr;
+    const int64_t nmb = mb ? dense_mbox_values(nt0) : 0;
+    const T mbv = pending_value<T>();
     const int n = (int)g.n0;
     const dim3 grid(cdiv(n, 16), cdiv(n, 16)), blk(16, 16);
     const T scale = (T)g.scale;
     const bool an = tb.aniso.grid != nullptr;
 #define GGP_ASM(DD)                                                                             \
     do {                                                                                        \
-        if (an) hipLaunchKernelGGL((k_dense_assemble<T, DD, true>), grid, blk, tb.aniso.lds, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso, zero_info, zero_info ? 1 : 0, zero_sync, nz1); \
-        else hipLaunchKernelGGL((k_dense_assemble<T, DD, false>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso, zero_info, zero_info ? 1 : 0, zero_sync, nz1); \
+        if (an) hipLaunchKernelGGL((k_dense_assemble<T, DD, true>), grid, blk, tb.aniso.lds, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso, zero_info, zero_info ? 1 : 0, zero_sync, nz1, mb, nmb, mbv); \
+        else hipLaunchKernelGGL((k_dense_assemble<T, DD, false>), grid, blk, 0, st, A, g.coords, n, scale, tb.tab, tb.acc, tb.params, diag_add, tb.aniso, zero_info, zero_info ? 1 : 0, zero_sync, nz1, mb, nmb, mbv); \
     } while (0)
     switch (g.D) {
         case 2: GGP_ASM(2); break;

@@ -149,51 +149,6 @@ k_factor(const uint32_t* __restrict__ coords, const int32_t* __restrict__ nbr, i
 // and no wavefront ever waits for a lane of its own. Every wait is bounded: past
 // kSweepSpinLimit polls it sets bit 2 of *err and goes on, so every workgroup exits; the host
 // reports that as an error. The arithmetic per point is the per-level kernels', unchanged.
-template <typename T> struct Pending;
-template <> struct Pending<float> { static constexpr uint32_t bits = 0x7fc0feedu; };
-template <> struct Pending<double> { static constexpr uint64_t bits = 0x7ff800000000feedull; };
-constexpr int kSweepSpinLimit = 1 << 20;
-
-__device__ inline float from_bits(uint32_t b) { return __uint_as_float(b); }
-__device__ inline double from_bits(uint64_t b) { return __longlong_as_double((long long)b); }
-
-// Values at p[idx[u]] for the live entries u < B (live[u] false: 0). All reads are issued
-// together; the ones still pending are polled together, one back-off sleep per round.
-template <typename T, int B>
-__device__ inline void sweep_read_all(T (&out)[B], const T* p, const int64_t (&idx)[B],
-                                      const bool (&live)[B], int* err) {
-    using U = typename num<T>::bits_t;
-    const U* pu = reinterpret_cast<const U*>(p);
-    U b[B];
-#pragma unroll
-    for (int u = 0; u < B; ++u) b[u] = live[u] ? pu[idx[u]] : U(0);
-    for (int spins = 0;; ++spins) {
-        bool pending = false;
-#pragma unroll
-        for (int u = 0; u < B; ++u) pending = pending || b[u] == Pending<T>::bits;
-        if (!pending) break;
-        if (spins > kSweepSpinLimit) {
-            atomicOr(err, 4);
-            break;
-        }
-        if (spins < 8) __builtin_amdgcn_s_sleep(1);
-        else __builtin_amdgcn_s_sleep(4);
-#pragma unroll
-        for (int u = 0; u < B; ++u)
-            if (b[u] == Pending<T>::bits)
-                b[u] = __hip_atomic_load(pu + idx[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-#pragma unroll
-    for (int u = 0; u < B; ++u) out[u] = live[u] ? from_bits(b[u]) : T(0);
-}
-
-template <typename T>
-__device__ inline void sweep_publish(T* p, T x) {
-    using U = typename num<T>::bits_t;
-    __hip_atomic_store(reinterpret_cast<U*>(p), num<T>::bits(x), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Next chunk for the workgroup; the value is made wave-uniform for the compiler (readfirstlane)
 // so the loop test is a uniform branch and the loop keeps its shape.
 __device__ inline int sweep_next(int* ticket, int* s_c) {
