@@ -410,9 +410,19 @@ __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[
             if (16 * h + u <= r) wp[u] = a[u];
         if (kRsq && diag_lane) dinv[j * kTile + r] = myinv;
     }
-    if (mbox) {  // the whole tile, row-major, value by value
+    if (mbox) {  // the whole tile, row-major, value by value (f32: two per 64-bit store)
+        if constexpr (sizeof(T) == 4) {
 #pragma unroll
-        for (int u = 0; u < 16; ++u) sweep_publish(&mbox[r * kTile + 16 * h + u], a[u]);
+            for (int u = 0; u < 16; u += 2) {
+                const uint64_t b2 = (uint64_t)__float_as_uint(a[u]) |
+                                    ((uint64_t)__float_as_uint(a[u + 1]) << 32);
+                __hip_atomic_store(reinterpret_cast<uint64_t*>(&mbox[r * kTile + 16 * h + u]), b2,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) sweep_publish(&mbox[r * kTile + 16 * h + u], a[u]);
+        }
     }
     if (kRsq && diag_lane) inv[r] = myinv;
     if (!STREAM) {
