@@ -405,9 +405,24 @@ __device__ __forceinline__ void walk_factor_t(T* A, int n, int j, const T (*sA)[
     const bool diag_lane = h == (r >> 4);  // holds L[r][r] (and its reciprocal)
     if (live) {
         T* wp = A + (int64_t)(j * kTile + r) * n + j * kTile + 16 * h;
+        if (sizeof(T) == 4 && (n & 1) == 0) {
+            // f32 rows of even length: pairs of columns in one 64-bit store where both are in
+            // the lower triangle
 #pragma unroll
-        for (int u = 0; u < 16; ++u)
-            if (16 * h + u <= r) wp[u] = a[u];
+            for (int u = 0; u < 16; u += 2) {
+                if (16 * h + u + 1 <= r) {
+                    const uint64_t b2 = (uint64_t)num<T>::bits(a[u]) |
+                                        ((uint64_t)num<T>::bits(a[u + 1]) << 32);
+                    *reinterpret_cast<uint64_t*>(wp + u) = b2;
+                } else if (16 * h + u == r) {
+                    wp[u] = a[u];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (16 * h + u <= r) wp[u] = a[u];
+        }
         if (kRsq && diag_lane) dinv[j * kTile + r] = myinv;
     }
     if (mbox) {  // the whole tile, row-major, value by value (f32: two per 64-bit store)
