@@ -890,14 +890,16 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
 //     finished tiles (i, k) and (s, k); workgroup 0 then factors the diagonal tile (the walker
 //     factor) and publishes it, and every other workgroup solves its tile against it (the walker
 //     solve). Workgroup 0 is dispatched first and waits for nothing, so the others' waits end.
-//   k_syrk_blk (one launch per super-panel): every kSyrkB x kSyrkB block of the trailing lower
+//   k_syrk_blk (one launch per super-panel): every 128 x 128 block of the trailing lower
 //     triangle receives the super-panel's kSuper*32 terms, k increasing, in register
-//     accumulators; the panel rows are staged in LDS a few columns at a time.
+//     accumulators; the panel rows are staged in LDS a few columns at a time. A block takes one
+//     workgroup about 60 us whatever the grid, so a trailing matrix of too few 128-blocks to
+//     give every CU two is cut into 64 x 64 blocks instead (four times the workgroups, a
+//     quarter of the work each; the terms and their order are the same).
 // Entry (r, c) thus receives the terms of earlier super-panels through k_syrk_blk, then those of
 // its own super-panel through k_panel_step, every one in increasing k: the unblocked chain, so
 // the factor is bit-identical to the persistent launches' and to the oracle's.
 constexpr int kSuper = 4;     // tile columns per super-panel (128 terms per trailing update)
-constexpr int kSyrkB = 128;   // trailing-update block edge
 constexpr int kBlockedMin = 2049;  // blocks of at least this many points take this path
 
 template <typename T>
@@ -953,14 +955,15 @@ __global__ void __launch_bounds__(kDfThreads) k_panel_step(T* __restrict__ A, in
 }
 
 // A[r][c] = fma(-A[r][k], A[c][k], A[r][c]) for k = k0, ..., k0 + kd - 1 over the lower blocks of
-// the trailing matrix (r, c >= t0), one kSyrkB x kSyrkB block per workgroup: thread (ty, tx)
-// holds rows ty*8 .. ty*8+7 and columns tx*8 .. tx*8+7 of it. Diagonal blocks are computed
-// whole; their upper part lies in the unused upper triangle of A.
-template <typename T>
+// the trailing matrix (r, c >= t0), one BS x BS block per workgroup: thread (ty, tx) holds rows
+// ty*TM .. ty*TM+TM-1 and columns tx*TM .. tx*TM+TM-1 of it (TM = BS/16). Diagonal blocks are
+// computed whole; their upper part lies in the unused upper triangle of A.
+template <typename T, int BS>
 __global__ void __launch_bounds__(256) k_syrk_blk(T* __restrict__ A, int n, int t0, int k0,
                                                   int kd) {
+    constexpr int TM = BS / 16;
     constexpr int Kc = sizeof(T) == 4 ? 32 : 16;  // panel columns per LDS round
-    constexpr int P = kSyrkB + 4;                 // row pitch: 16-byte aligned rows
+    constexpr int P = BS + 4;                     // row pitch: 16-byte aligned rows
     __shared__ __align__(16) T sa[Kc][P];         // sa[k][r] = A[R0 + r][k0 + kc + k]
     __shared__ __align__(16) T sb[Kc][P];         // sb[k][c] = A[C0 + c][k0 + kc + k]
     const int L = (int)blockIdx.x;
@@ -968,22 +971,22 @@ __global__ void __launch_bounds__(256) k_syrk_blk(T* __restrict__ A, int n, int 
     while ((I + 1) * (I + 2) / 2 <= L) ++I;
     while (I * (I + 1) / 2 > L) --I;
     const int J = L - I * (I + 1) / 2;
-    const int R0 = t0 + I * kSyrkB, C0 = t0 + J * kSyrkB;
+    const int R0 = t0 + I * BS, C0 = t0 + J * BS;
     const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
-    T acc[8][8];
+    T acc[TM][TM];
 #pragma unroll
-    for (int a = 0; a < 8; ++a) {
-        const int r = R0 + ty * 8 + a;
+    for (int a = 0; a < TM; ++a) {
+        const int r = R0 + ty * TM + a;
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const int cc = C0 + tx * 8 + b;
+        for (int b = 0; b < TM; ++b) {
+            const int cc = C0 + tx * TM + b;
             acc[a][b] = (r < n && cc < n) ? A[(int64_t)r * n + cc] : T(0);
         }
     }
     for (int kc = 0; kc < kd; kc += Kc) {
         __syncthreads();
         // rows of the two panels, Kc consecutive columns each (k fastest: coalesced)
-        for (int e = tid; e < kSyrkB * Kc; e += 256) {
+        for (int e = tid; e < BS * Kc; e += 256) {
             const int r = e / Kc, k = e - r * Kc;
             const int64_t col = (int64_t)k0 + kc + k;
             sa[k][r] = R0 + r < n ? A[(int64_t)(R0 + r) * n + col] : T(0);
@@ -992,23 +995,23 @@ __global__ void __launch_bounds__(256) k_syrk_blk(T* __restrict__ A, int n, int 
         __syncthreads();
 #pragma unroll 4
         for (int k = 0; k < Kc; ++k) {
-            T x[8], y[8];
+            T x[TM], y[TM];
 #pragma unroll
-            for (int a = 0; a < 8; ++a) x[a] = sa[k][ty * 8 + a];
+            for (int a = 0; a < TM; ++a) x[a] = sa[k][ty * TM + a];
 #pragma unroll
-            for (int b = 0; b < 8; ++b) y[b] = sb[k][tx * 8 + b];
+            for (int b = 0; b < TM; ++b) y[b] = sb[k][tx * TM + b];
 #pragma unroll
-            for (int a = 0; a < 8; ++a)
+            for (int a = 0; a < TM; ++a)
 #pragma unroll
-                for (int b = 0; b < 8; ++b) acc[a][b] = num<T>::fma(-x[a], y[b], acc[a][b]);
+                for (int b = 0; b < TM; ++b) acc[a][b] = num<T>::fma(-x[a], y[b], acc[a][b]);
         }
     }
 #pragma unroll
-    for (int a = 0; a < 8; ++a) {
-        const int r = R0 + ty * 8 + a;
+    for (int a = 0; a < TM; ++a) {
+        const int r = R0 + ty * TM + a;
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const int cc = C0 + tx * 8 + b;
+        for (int b = 0; b < TM; ++b) {
+            const int cc = C0 + tx * TM + b;
             if (r < n && cc < n) A[(int64_t)r * n + cc] = acc[a][b];
         }
     }
@@ -1023,6 +1026,9 @@ bool dense_blocked(int n) {
 template <typename T>
 void dense_potrf_blocked(T* A, int n, int* info, int* flags, hipStream_t st) {
     const int nt = (n + kTile - 1) / kTile;
+    int dev = 0, ncu = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
     for (int s0 = 0; s0 < nt; s0 += kSuper) {
         const int s1 = std::min(nt, s0 + kSuper);
         for (int s = s0; s < s1; ++s)
@@ -1030,9 +1036,17 @@ void dense_potrf_blocked(T* A, int n, int* info, int* flags, hipStream_t st) {
                                s0, flags + s, info);
         const int t0 = s1 * kTile;
         if (t0 < n) {
-            const int mb = (n - t0 + kSyrkB - 1) / kSyrkB;
-            hipLaunchKernelGGL((k_syrk_blk<T>), dim3(mb * (mb + 1) / 2), dim3(256), 0, st, A, n,
-                               t0, s0 * kTile, (s1 - s0) * kTile);
+            const int mb = (n - t0 + 127) / 128;
+            const char* force = std::getenv("GGP_SYRK_BLOCK");  // "64" / "128" forces the edge
+            const bool big = force ? std::atoi(force) == 128 : mb * (mb + 1) / 2 >= 2 * ncu;
+            if (big) {
+                hipLaunchKernelGGL((k_syrk_blk<T, 128>), dim3(mb * (mb + 1) / 2), dim3(256), 0,
+                                   st, A, n, t0, s0 * kTile, (s1 - s0) * kTile);
+            } else {
+                const int m64 = (n - t0 + 63) / 64;
+                hipLaunchKernelGGL((k_syrk_blk<T, 64>), dim3(m64 * (m64 + 1) / 2), dim3(256), 0,
+                                   st, A, n, t0, s0 * kTile, (s1 - s0) * kTile);
+            }
         }
     }
 }
