@@ -918,18 +918,33 @@ __global__ void __launch_bounds__(kDfThreads) k_panel_step(T* __restrict__ A, in
     T acc[4];
     walk_load(acc, A, n, i, s, r0, c);
     // the super-panel's finished columns (tiles k < s, all full: only the last tile column can
-    // be partial), rows past n read as zero
-    for (int k = s0; k < s; ++k) {
-        const int kk = k * kTile;
+    // be partial), rows past n read as zero; all their loads are issued first, so the tiles
+    // cost one round trip together, and the terms are then added tile by tile, k increasing
+    T xa[kSuper - 1][4], xb[kSuper - 1][4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int r = r0 + 8 * q;
-            sA[r][c] = i0 + r < n ? A[(int64_t)(i0 + r) * n + kk + c] : T(0);
-            sB[r][c] = s0r + r < n ? A[(int64_t)(s0r + r) * n + kk + c] : T(0);
+    for (int u = 0; u < kSuper - 1; ++u) {
+        if (s0 + u < s) {
+            const int kk = (s0 + u) * kTile;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = r0 + 8 * q;
+                xa[u][q] = i0 + r < n ? A[(int64_t)(i0 + r) * n + kk + c] : T(0);
+                xb[u][q] = s0r + r < n ? A[(int64_t)(s0r + r) * n + kk + c] : T(0);
+            }
         }
-        __syncthreads();
-        walk_term(acc, sA, sB, r0, c);
-        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < kSuper - 1; ++u) {
+        if (s0 + u < s) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                sA[r0 + 8 * q][c] = xa[u][q];
+                sB[r0 + 8 * q][c] = xb[u][q];
+            }
+            __syncthreads();
+            walk_term(acc, sA, sB, r0, c);
+            __syncthreads();
+        }
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) sA[r0 + 8 * q][c] = acc[q];
