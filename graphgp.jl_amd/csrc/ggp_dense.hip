@@ -884,14 +884,14 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
 // ---- the same factor for large blocks: a few launches per tile column --------------------------
 // In the persistent launches above every 32 x 32 tile re-reads two input tiles per 32 terms, so
 // at a few thousand points the helpers' tile traffic and hand-offs, not arithmetic, set the
-// time. For large blocks the matrix is instead swept in super-panels of kSuper tile columns:
+// time. For large blocks the matrix is instead swept in super-panels of 4 or 8 tile columns:
 //   k_panel_step (one launch per tile column s of the super-panel): workgroup i - s takes tile
 //     (i, s), adds the terms of the super-panel's earlier columns k in [32*s0, 32*s) from the
 //     finished tiles (i, k) and (s, k); workgroup 0 then factors the diagonal tile (the walker
 //     factor) and publishes it, and every other workgroup solves its tile against it (the walker
 //     solve). Workgroup 0 is dispatched first and waits for nothing, so the others' waits end.
 //   k_syrk_blk (one launch per super-panel): every 128 x 128 block of the trailing lower
-//     triangle receives the super-panel's kSuper*32 terms, k increasing, in register
+//     triangle receives the super-panel's 128 or 256 terms, k increasing, in register
 //     accumulators; the panel rows are staged in LDS a few columns at a time. A block takes one
 //     workgroup about 60 us whatever the grid, so a trailing matrix of too few 128-blocks to
 //     give every CU two is cut into 64 x 64 blocks instead (four times the workgroups, a
@@ -899,7 +899,11 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
 // Entry (r, c) thus receives the terms of earlier super-panels through k_syrk_blk, then those of
 // its own super-panel through k_panel_step, every one in increasing k: the unblocked chain, so
 // the factor is bit-identical to the persistent launches' and to the oracle's.
-constexpr int kSuper = 4;     // tile columns per super-panel (128 terms per trailing update)
+// Tile columns per super-panel: 8 from kSuperWideMin points (half the trailing-update launches,
+// twice the terms per accumulator load: 94 against 103 ms at 16384 points), 4 below (at 4096
+// points the wider panels' longer panel steps cost more: 4.7 against 4.3 ms).
+constexpr int kSuper = 8;             // the widest super-panel
+constexpr int kSuperWideMin = 8192;
 constexpr int kBlockedMin = 2049;  // blocks of at least this many points take this path
 
 template <typename T>
@@ -1041,11 +1045,14 @@ bool dense_blocked(int n) {
 template <typename T>
 void dense_potrf_blocked(T* A, int n, int* info, int* flags, hipStream_t st) {
     const int nt = (n + kTile - 1) / kTile;
+    const char* fs = std::getenv("GGP_POTRF_SUPER");  // "4" / "8" forces the width
+    const int ks = fs ? (std::atoi(fs) == 8 ? kSuper : kSuper / 2)
+                      : (n >= kSuperWideMin ? kSuper : kSuper / 2);
     int dev = 0, ncu = 256;
     if (hipGetDevice(&dev) == hipSuccess)
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
-    for (int s0 = 0; s0 < nt; s0 += kSuper) {
-        const int s1 = std::min(nt, s0 + kSuper);
+    for (int s0 = 0; s0 < nt; s0 += ks) {
+        const int s1 = std::min(nt, s0 + ks);
         for (int s = s0; s < s1; ++s)
             hipLaunchKernelGGL((k_panel_step<T>), dim3(nt - s), dim3(kDfThreads), 0, st, A, n, s,
                                s0, flags + s, info);

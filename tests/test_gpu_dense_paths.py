@@ -5,8 +5,8 @@ column-by-column factor.
 Both schedules give every entry of the factor the unblocked left-looking fma chain in the same
 order, so the dense part of generate (L xi, a product whose chain is also the oracle's) must
 have the oracle's bits in Float32 and Float64, whichever schedule ran. GGP_POTRF_BLOCKED forces
-the schedule and GGP_SYRK_BLOCK the blocked path's trailing-update block edge, 64 or 128 (both
-read at every call).
+the schedule, GGP_SYRK_BLOCK the blocked path's trailing-update block edge (64 or 128) and
+GGP_POTRF_SUPER its super-panel width (4 or 8 tile columns), all read at every call.
 """
 import sys
 
@@ -53,24 +53,26 @@ def test_blocked_and_walker_factor_bit_exact(gpu, monkeypatch, n0, dtype):
     want = ref.generate(xi)
     ld_want = ref.generate_logdet()
     out = {}
-    for mode, blk in (("0", "64"), ("1", "64"), ("1", "128")):
+    for mode, blk, sup in (("0", "64", "4"), ("1", "64", "4"), ("1", "128", "4"),
+                           ("1", "64", "8")):
         monkeypatch.setenv("GGP_POTRF_BLOCKED", mode)
         monkeypatch.setenv("GGP_SYRK_BLOCK", blk)
+        monkeypatch.setenv("GGP_POTRF_SUPER", sup)
         f = G().generate(hp, xi)
         ld = G().generate_logdet(hp)
-        _say(f"  blocked={mode} block={blk}: generate relerr {relerr(f, want):.3e}, "
+        _say(f"  blocked={mode} block={blk} super={sup}: generate relerr {relerr(f, want):.3e}, "
              f"logdet {abs(ld - ld_want) / abs(ld_want):.3e}")
         np.testing.assert_array_equal(f, want)
         assert abs(ld - ld_want) <= (1e-12 if dtype == np.float64 else 1e-5) * abs(ld_want)
-        out[mode + blk] = f
-    np.testing.assert_array_equal(out["064"], out["164"])
-    np.testing.assert_array_equal(out["064"], out["1128"])
+        out[mode + blk + sup] = f
+    for key in ("1644", "11284", "1648"):
+        np.testing.assert_array_equal(out["0644"], out[key])
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_trailing_update_blocks_agree_at_4160(gpu, monkeypatch, dtype):
-    """At 4160 dense points (the blocked schedule by default) the two trailing-update block
-    edges give the same bits, the oracle's (the oracle's factor takes a few seconds at this
+    """At 4160 dense points (the blocked schedule by default) both trailing-update block edges
+    and both super-panel widths give the same bits, the oracle's (the oracle's factor takes a few seconds at this
     size, so it is run once)."""
     _say(f"case trailing-update blocks n0=4160 {np.dtype(dtype).name}")
     prob, ref, rng = _problem(4800, 4160, dtype, seed=4160)
@@ -78,10 +80,12 @@ def test_trailing_update_blocks_agree_at_4160(gpu, monkeypatch, dtype):
     xi = rng.standard_normal(prob.N).astype(dtype)
     monkeypatch.delenv("GGP_POTRF_BLOCKED", raising=False)
     out = {}
-    for blk in ("64", "128"):
+    for blk, sup in (("64", "4"), ("128", "4"), ("128", "8")):
         monkeypatch.setenv("GGP_SYRK_BLOCK", blk)
-        out[blk] = G().generate(hp, xi)
-    np.testing.assert_array_equal(out["64"], out["128"])
+        monkeypatch.setenv("GGP_POTRF_SUPER", sup)
+        out[blk] = out[blk + sup] = G().generate(hp, xi)
+    np.testing.assert_array_equal(out["644"], out["1284"])
+    np.testing.assert_array_equal(out["644"], out["1288"])
     want = ref.generate(xi)
     _say(f"  generate relerr vs oracle {relerr(out['64'], want):.3e}")
     np.testing.assert_array_equal(out["64"], want)
