@@ -899,10 +899,11 @@ __global__ void __launch_bounds__(kDfThreads) __attribute__((amdgpu_waves_per_eu
 // Entry (r, c) thus receives the terms of earlier super-panels through k_syrk_blk, then those of
 // its own super-panel through k_panel_step, every one in increasing k: the unblocked chain, so
 // the factor is bit-identical to the persistent launches' and to the oracle's.
-// Tile columns per super-panel: 8 from kSuperWideMin points (half the trailing-update launches,
-// twice the terms per accumulator load: 94 against 103 ms at 16384 points), 4 below (at 4096
-// points the wider panels' longer panel steps cost more: 4.7 against 4.3 ms).
-constexpr int kSuper = 8;             // the widest super-panel
+// Tile columns per super-panel: 4 below kSuperWideMin points, 8 from there and 16 from twice
+// that. Wider panels halve the trailing-update launches and double the terms per accumulator
+// load (16384 points: 103 ms with 4, 94 with 8, 90 with 16), but lengthen the panel steps,
+// which costs more at a few thousand points (4096: 4.3 ms with 4, 4.7 with 8).
+constexpr int kSuper = 16;            // the widest super-panel
 constexpr int kSuperWideMin = 8192;
 constexpr int kBlockedMin = 2049;  // blocks of at least this many points take this path
 
@@ -1045,9 +1046,11 @@ bool dense_blocked(int n) {
 template <typename T>
 void dense_potrf_blocked(T* A, int n, int* info, int* flags, hipStream_t st) {
     const int nt = (n + kTile - 1) / kTile;
-    const char* fs = std::getenv("GGP_POTRF_SUPER");  // "4" / "8" forces the width
-    const int ks = fs ? (std::atoi(fs) == 8 ? kSuper : kSuper / 2)
-                      : (n >= kSuperWideMin ? kSuper : kSuper / 2);
+    const char* fs = std::getenv("GGP_POTRF_SUPER");  // "4" / "8" / "16" forces the width
+    const int fw = fs ? std::atoi(fs) : 0;
+    const int ks = (fw == 4 || fw == 8 || fw == 16)
+                       ? fw
+                       : (n >= 2 * kSuperWideMin ? 16 : n >= kSuperWideMin ? 8 : 4);
     int dev = 0, ncu = 256;
     if (hipGetDevice(&dev) == hipSuccess)
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);

@@ -6,7 +6,7 @@ Both schedules give every entry of the factor the unblocked left-looking fma cha
 order, so the dense part of generate (L xi, a product whose chain is also the oracle's) must
 have the oracle's bits in Float32 and Float64, whichever schedule ran. GGP_POTRF_BLOCKED forces
 the schedule, GGP_SYRK_BLOCK the blocked path's trailing-update block edge (64 or 128) and
-GGP_POTRF_SUPER its super-panel width (4 or 8 tile columns), all read at every call.
+GGP_POTRF_SUPER its super-panel width (4, 8 or 16 tile columns), all read at every call.
 """
 import sys
 
@@ -54,7 +54,7 @@ def test_blocked_and_walker_factor_bit_exact(gpu, monkeypatch, n0, dtype):
     ld_want = ref.generate_logdet()
     out = {}
     for mode, blk, sup in (("0", "64", "4"), ("1", "64", "4"), ("1", "128", "4"),
-                           ("1", "64", "8")):
+                           ("1", "64", "8"), ("1", "128", "16")):
         monkeypatch.setenv("GGP_POTRF_BLOCKED", mode)
         monkeypatch.setenv("GGP_SYRK_BLOCK", blk)
         monkeypatch.setenv("GGP_POTRF_SUPER", sup)
@@ -65,7 +65,7 @@ def test_blocked_and_walker_factor_bit_exact(gpu, monkeypatch, n0, dtype):
         np.testing.assert_array_equal(f, want)
         assert abs(ld - ld_want) <= (1e-12 if dtype == np.float64 else 1e-5) * abs(ld_want)
         out[mode + blk + sup] = f
-    for key in ("1644", "11284", "1648"):
+    for key in ("1644", "11284", "1648", "112816"):
         np.testing.assert_array_equal(out["0644"], out[key])
 
 
@@ -80,12 +80,13 @@ def test_trailing_update_blocks_agree_at_4160(gpu, monkeypatch, dtype):
     xi = rng.standard_normal(prob.N).astype(dtype)
     monkeypatch.delenv("GGP_POTRF_BLOCKED", raising=False)
     out = {}
-    for blk, sup in (("64", "4"), ("128", "4"), ("128", "8")):
+    for blk, sup in (("64", "4"), ("128", "4"), ("128", "8"), ("64", "16")):
         monkeypatch.setenv("GGP_SYRK_BLOCK", blk)
         monkeypatch.setenv("GGP_POTRF_SUPER", sup)
         out[blk] = out[blk + sup] = G().generate(hp, xi)
     np.testing.assert_array_equal(out["644"], out["1284"])
     np.testing.assert_array_equal(out["644"], out["1288"])
+    np.testing.assert_array_equal(out["644"], out["6416"])
     want = ref.generate(xi)
     _say(f"  generate relerr vs oracle {relerr(out['64'], want):.3e}")
     np.testing.assert_array_equal(out["64"], want)
