@@ -112,3 +112,41 @@ def test_blocked_factor_not_positive_definite_retry(gpu, monkeypatch):
         res[mode] = G().generate(hp, xi)
         assert np.all(np.isfinite(res[mode]))
     np.testing.assert_array_equal(res["0"], res["1"])
+
+
+def test_every_op_on_the_blocked_schedule(gpu, monkeypatch):
+    """Every op that factors the dense block gives the walker schedule's results when the
+    blocked schedule runs instead: the same factor bits, so equal fields and solves, and
+    gradients equal up to the order of their f64 sums."""
+    _say("case every op on the blocked schedule")
+    prob, ref, rng = _problem(1500, 600, np.float64, seed=21)
+    hp = G().to_backend(prob)
+    xi = rng.standard_normal(prob.N)
+    vbar = rng.standard_normal(prob.N)
+    data = rng.standard_normal(prob.N)
+    ops = {
+        "generate": lambda: G().generate(hp, xi),
+        "generate_inv": lambda: G().generate_inv(hp, data),
+        "generate_logdet": lambda: np.array([G().generate_logdet(hp)]),
+        "generate_grad_xi": lambda: G().generate_grad_xi(hp, vbar),
+        "generate_grad_vals": lambda: G().generate_grad_vals(hp, xi, vbar),
+        "generate_logdet_grad_vals": lambda: G().generate_logdet_grad_vals(hp),
+        "generate_inv_loss_grad_vals": lambda: G().generate_inv_loss_grad_vals(hp, data),
+        "generate_logdet_grad_points": lambda: G().generate_logdet_grad_points(hp),
+    }
+    def flat(r):
+        parts = r if isinstance(r, (tuple, list)) else (r,)
+        return np.concatenate([np.ravel(np.asarray(x, dtype=np.float64)) for x in parts])
+
+    res = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("GGP_POTRF_BLOCKED", mode)
+        res[mode] = {k: flat(f()) for k, f in ops.items()}
+    for k in ops:
+        a, b = res["0"][k], res["1"][k]
+        err = relerr(b, a)
+        _say(f"  {k}: blocked vs walker relerr {err:.3e}")
+        if k in ("generate", "generate_inv", "generate_grad_xi"):
+            np.testing.assert_array_equal(a, b)
+        else:
+            assert err < 1e-12, k
